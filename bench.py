@@ -1,0 +1,221 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X verify hot path on one GPU.
+
+Headline (one JSON line on stdout): paged verify attention of one Qwen3-8B-shaped layer (32 q / 8 kv heads,
+head_dim 128, bf16, 256-token pages) at batch 64 with verify lengths uniform in {1..8} (tokens padded to a multiple
+of 8 with a padding row on the zero pad block) and contexts uniform in [2800, 3200]; max_seqlen_k = 4096 as the
+verify graphs pass it. value = algorithmic HBM bytes (every visible K/V row once + q + out) / time per layer.
+
+Also measured: the fused speculative sampler (64 rows x 8 verified positions, V = 151,936, fp32 logits ~ N(0, 9),
+top-k 64), against the one read of the [512, V] logits it must make; and the torch-CPU restatement of the same
+attention (the oracle, the reference's CPU path) on the host cores as a reported baseline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-baseline on|off] [--sampler on|off]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "verify-attn µs/layer & HBM GB/s (% of 8 TB/s) at B=64, 8 q, 3k ctx"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_gpu(fn, steps: int, warmup: int):
+    """Average ms per call of fn over `steps` calls after `warmup`, bracketed by HIP events on the current
+    stream (the stream the kernels are launched on) and device synchronisations on both sides."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_cpu(fn, budget_s: float = 15.0, max_runs: int = 10):
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < max_runs and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def attention_bench(args, dev):
+    import torch
+
+    import nvs_amd.workloads as wl
+    from nvs_amd.layers import attention as nattn
+
+    log("[bench] building the batch-64 verify-attention workload")
+    case = wl.config_c3()
+    g = case.to(dev)
+    max_k = 4096
+    out = torch.empty_like(g.q)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+
+    def step():
+        nattn._paged_attention(g.q, g.k_cache, g.v_cache, g.block_tables, g.cu_seqlens_q, g.cu_seqlens_k, None, 0,
+                               len(case.q_lens), g.max_seqlen_q, max_k, g.scale, True, out=out, workspace=ws)
+
+    ms = time_gpu(step, args.steps, args.warmup)
+    kv, qo = case.kv_bytes(), case.qo_bytes()
+    gbs = (kv + qo) / (ms * 1e-3) / 1e9
+    flops = case.flops()
+    log(f"[bench] attention: {ms * 1e3:.1f} us/layer, {gbs:.0f} GB/s = {100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
+    return case, ms, kv + qo, gbs, flops
+
+
+def launch_bound_bench(args, dev):
+    """The batch-8 shape (contexts 900-1200): too small to fill the chip; reported, not a target."""
+    import torch
+
+    import nvs_amd.workloads as wl
+    from nvs_amd.layers import attention as nattn
+    case = wl.config_c2()
+    g = case.to(dev)
+    out = torch.empty_like(g.q)
+    ws = torch.empty(16 << 20, dtype=torch.uint8, device=dev)
+
+    def step():
+        nattn._paged_attention(g.q, g.k_cache, g.v_cache, g.block_tables, g.cu_seqlens_q, g.cu_seqlens_k, None, 0,
+                               len(case.q_lens), g.max_seqlen_q, 4096, g.scale, True, out=out, workspace=ws)
+
+    ms = time_gpu(step, args.steps, args.warmup)
+    b = case.kv_bytes() + case.qo_bytes()
+    return {"workload": "verify_attention_qwen3_8b_b8_ctx900_1200", "us": round(ms * 1e3, 2),
+            "GBs": round(b / (ms * 1e-3) / 1e9, 1), "bytes": b}
+
+
+def sampler_bench(args, dev):
+    import torch
+
+    import nvs_amd.workloads as wl
+    from nvs_amd.layers import spec_sampler as ns
+
+    def draft_probs(lg, t, k, p):
+        # top-64 softmax of the draft logits (every row has top_k 64, temperature 1)
+        s = lg / t[:, None, None]
+        kth = s.topk(64, dim=-1).values[..., -1:]
+        return torch.softmax(s.masked_fill(s < kth, float("-inf")), dim=-1)
+
+    log("[bench] building the 64 x 8 x 151936 sampler workload")
+    case = wl.sampler_case(64, 7, 151936, draft_probs_fn=draft_probs)
+    g = case.to(dev)
+    st = ns.SamplingTensors(g.temperatures, g.top_k, g.top_p, case.max_top_k, case.has_top_p, True)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+
+    def step():
+        ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st, None, g.uniforms, g.noise, workspace=ws)
+
+    ms = time_gpu(step, max(10, args.steps // 2), max(3, args.warmup // 2))
+    T, V = case.logits.shape
+    alg = T * V * 4
+    gbs = alg / (ms * 1e-3) / 1e9
+    n, tail = step_out = ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st, None, g.uniforms, g.noise,
+                                                   workspace=ws)
+    torch.cuda.synchronize()
+    del step_out
+    log(f"[bench] fused sampler: {ms * 1e3:.1f} us, {gbs:.0f} GB/s = {100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
+    return {"workload": "spec_accept_b64_k7_v151936_fp32_topk64", "us": round(ms * 1e3, 2),
+            "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": alg,
+            "mean_accepted": round(float(n.float().mean()), 3)}
+
+
+def cpu_baseline(case):
+    """The torch-CPU restatement of the reference's paged attention (oracle), in fp32 on the host cores, over the
+    whole batch-64 layer (inputs converted to fp32 before timing)."""
+    import torch
+
+    from oracle import attention as ref
+    torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+    q = case.q.float()
+    kc = case.k_cache.float()
+    vc = case.v_cache.float()
+    rows = case.rows
+
+    def run():
+        ref.paged_attention_t32(q, kc, vc, case.block_tables, rows, case.scale, True)
+
+    sec, runs = time_cpu(run)
+    gbs = (case.kv_bytes() + case.qo_bytes()) / sec / 1e9
+    log(f"[bench] cpu baseline: {sec * 1e3:.1f} ms/layer on {torch.get_num_threads()} threads")
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"the whole batch-64 layer (same inputs as the GPU run, fp32), median of {runs} runs: "
+                      f"{sec * 1e3:.1f} ms/layer", "ms_per_layer": round(sec * 1e3, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    ap.add_argument("--sampler", choices=["on", "off"], default="on")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the verify hot path runs on one GPU's share and this build has no "
+              "multi-GPU path; run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import nvs_amd  # noqa: F401
+    from nvs_amd import _lib
+    _lib.load()
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm device", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+
+    case, ms, nbytes, gbs, flops = attention_bench(args, dev)
+    extra = {"c2": launch_bound_bench(args, dev)}
+    if args.sampler == "on":
+        extra["sampler"] = sampler_bench(args, dev)
+    cpu = cpu_baseline(case) if args.cpu_baseline == "on" else None
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200",
+                   "rows": len(case.q_lens), "tokens": int(sum(case.q_lens)), "heads": "32q/8kv",
+                   "head_dim": 128, "block_size": 256, "max_seqlen_k": 4096},
+        "us_per_layer": round(ms * 1e3, 2),
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": nbytes,
+                     "kernel": "attn_split_kernel + attn_combine_kernel (one paged_attention call)"},
+        "mfma_tflops_useful": round(flops / (ms * 1e-3) / 1e12, 2),
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

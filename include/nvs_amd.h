@@ -1,0 +1,178 @@
+/*
+ * nvs_amd.h -- C ABI of the MI355X (gfx950) target-verify hot path of nano-vllm-speculative-decoding.
+ *
+ * Two ops live behind this boundary:
+ *   1. paged multi-query verify attention (+ the paged KV store that precedes it), and
+ *   2. the speculative sampler: truncation -> softmax -> rejection test -> residual / bonus race.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, plus the HIP stream to launch on
+ * (NULL = the legacy default stream). Nothing here allocates, synchronises the host with the device, or reads a
+ * device value on the host, so every call is safe inside HIP-graph capture when its workspace is preallocated.
+ *
+ * Return value: NVS_OK (0) or a negative nvs_status. On failure nvs_last_error() returns a message describing it
+ * (thread-local; valid until the next call on the same thread). Argument errors are detected on the host before any
+ * launch, so they are testable without a GPU.
+ *
+ * Strides are in ELEMENTS, not bytes. Token ids, lengths and counts follow the reference's dtypes: int32 for the
+ * attention metadata (cu_seqlens, context_lens, block_tables, slot_mapping), int64 for drafts, top_k,
+ * verified_lens and the sampler outputs.
+ */
+#ifndef NVS_AMD_H
+#define NVS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NVS_ABI_VERSION 1
+
+typedef enum {
+    NVS_OK = 0,
+    NVS_ERR_INVALID = -1,      /* bad argument: shape, stride, alignment, null pointer */
+    NVS_ERR_UNSUPPORTED = -2,  /* valid for the reference but not implemented by this library (e.g. head_dim 96) */
+    NVS_ERR_WORKSPACE = -3,    /* workspace missing or smaller than the matching *_workspace_size */
+    NVS_ERR_HIP = -4           /* the HIP runtime reported an error at launch */
+} nvs_status;
+
+typedef enum {
+    NVS_DTYPE_F32 = 0,
+    NVS_DTYPE_BF16 = 1,
+    NVS_DTYPE_F16 = 2
+} nvs_dtype;
+
+/* Version of this header's ABI; the Python loader refuses a library whose version differs. */
+int nvs_abi_version(void);
+
+/* Message of the last failed call on this thread ("" when none). */
+const char* nvs_last_error(void);
+
+/* ------------------------------------------------------------------------------------------------ KV store
+ * Replaces store_kvcache / store_kvcache_kernel (nanovllm/layers/attention.py:10-40; semantics restated in
+ * tests/fake_paged_attention.py:14-17).
+ * For i < n_tokens with s = slot_mapping[i] >= 0 (the reference skips exactly s == -1; negative slots and slots
+ * >= cache_slots are skipped here too instead of writing out of bounds):
+ *   k_cache[s*row + e] = key[i*key_row_stride + e], v_cache[s*row + e] = value[i*value_row_stride + e],
+ * for e < row = n_kv_heads*head_dim. Each token row of key/value must be contiguous (the reference asserts
+ * stride(-1) == 1 and stride(1) == head_dim); value may be a strided view (a slice of the fused qkv output).
+ * The caches are [cache_slots/block_size, block_size, n_kv_heads, head_dim] with contiguous slots. A pure copy:
+ * bit-exact for every dtype. */
+int nvs_store_kvcache(const void* key, int64_t key_row_stride,
+                      const void* value, int64_t value_row_stride,
+                      void* k_cache, void* v_cache, int64_t cache_slots,
+                      const int32_t* slot_mapping, int64_t n_tokens,
+                      int n_kv_heads, int head_dim, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ attention
+ * Replaces both flash-attn calls of Attention.forward (nanovllm/layers/attention.py:59-77):
+ *   varlen mode  (cu_seqlens_q and cu_seqlens_k non-NULL) = flash_attn_varlen_func(..., causal=True,
+ *                block_table=block_tables) of the verify / cached-prefix branch (attention.py:64-70);
+ *   fixed mode   (both NULL, context_lens non-NULL)      = flash_attn_with_kvcache(q.view(-1, query_len_per_seq, H,
+ *                D), cache_seqlens=context_lens, causal=causal) of the decode / draft-block branch (attention.py:71-76).
+ * Row r owns Lq query tokens starting at token q0 (varlen: q0 = cu_seqlens_q[r], Lq = cu_seqlens_q[r+1]-q0;
+ * fixed: q0 = r*query_len_per_seq, Lq = query_len_per_seq) and Lk keys (cu_seqlens_k[r+1]-cu_seqlens_k[r] or
+ * context_lens[r]); key j lives at k_cache[block_tables[r*bt_row_stride + j/block_size], j%block_size, g].
+ * Query i (< Lq) of head h attends to keys j < Lk, and with causal only to j <= Lk - Lq + i (bottom-right
+ * alignment), through kv head g = h / (n_heads/n_kv_heads):
+ *   out[q0+i, h] = softmax_j(scale * q[q0+i, h] . K_j) V_j, fp32 softmax and accumulation, bf16 out.
+ * Rows with Lq = 0 write nothing; a query that sees no key gets zeros.
+ * q and out are [n_tokens, n_heads, head_dim] with the given token/head strides; both caches share the strides
+ * [blocks, block_size, n_kv_heads, head_dim]. Supported here: dtype bf16, head_dim 128, block_size a multiple of 32,
+ * (n_heads/n_kv_heads)*max_seqlen_q any size (packed into 32-row tiles). max_seqlen_k bounds every Lk (the graph
+ * capture passes max_model_len); the grid depends only on the host integers, so a captured launch stays valid for
+ * any device lengths within those bounds.
+ * workspace: device memory of at least nvs_paged_attention_workspace_size(...) bytes (may be NULL when that is 0);
+ * no initialisation needed.
+ * Bounds: n_tokens (rows of q / out), cache_blocks (blocks of each cache) and bt_width (valid entries per block
+ * table row) bound every index the kernel derives from device metadata; inconsistent metadata gives wrong
+ * numbers for the rows concerned, never an access outside the buffers. */
+int nvs_paged_attention_workspace_size(int n_rows, int n_heads, int n_kv_heads, int head_dim,
+                                       int max_seqlen_q, int max_seqlen_k, size_t* bytes);
+
+int nvs_paged_attention(const void* q, int64_t q_token_stride, int64_t q_head_stride, int64_t n_tokens,
+                        const void* k_cache, const void* v_cache, int64_t cache_blocks,
+                        int64_t cache_block_stride, int64_t cache_token_stride, int64_t cache_head_stride,
+                        const int32_t* block_tables, int64_t bt_row_stride, int bt_width,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                        const int32_t* context_lens, int query_len_per_seq,
+                        int n_rows, int max_seqlen_q, int max_seqlen_k,
+                        int n_heads, int n_kv_heads, int head_dim, int block_size,
+                        float scale, int causal, int dtype,
+                        void* out, int64_t out_token_stride, int64_t out_head_stride,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ sampler
+ * Shared conventions (nanovllm/layers/spec_sampler.py):
+ *   logits are [n_pos, V] rows with row stride logits_row_stride, dtype f32/bf16/f16, upcast to fp32;
+ *   per-row sampling parameters (SamplingTensors, spec_sampler.py:17-24) are indexed by param row
+ *   pos / pos_per_param: temperatures f32 (divided into the logits, IEEE division), top_k int64 (0 = off),
+ *   top_p f32 (1 = off); max_top_k and has_top_p are the host flags of SamplingTensors.
+ *   Truncation = truncate_logits (spec_sampler.py:72-96): keep s >= threshold, ties kept, HuggingFace order
+ *   temperature -> top-k -> top-p-within-top-k; probabilities = softmax over the kept set.
+ * max_top_k above 1024 is NVS_ERR_UNSUPPORTED. */
+
+/* probs_from_logits (spec_sampler.py:65-69): dense fp32 probabilities [n_pos, V] into probs (row stride V). */
+int nvs_probs_from_logits_workspace_size(int64_t n_pos, int64_t vocab, int max_top_k, size_t* bytes);
+int nvs_probs_from_logits(const void* logits, int logits_dtype, int64_t logits_row_stride,
+                          int64_t n_pos, int64_t vocab, int64_t pos_per_param,
+                          const float* temperatures, const int64_t* top_k, const float* top_p,
+                          int max_top_k, int has_top_p,
+                          float* probs, void* workspace, size_t workspace_bytes, void* stream);
+
+/* truncate_logits (spec_sampler.py:72-96) of already temperature-scaled fp32 logits: out = scaled, or -inf below
+ * each row's threshold. out may alias scaled. */
+int nvs_truncate_logits(const float* scaled, int64_t scaled_row_stride, int64_t n_pos, int64_t vocab,
+                        int64_t pos_per_param, const int64_t* top_k, const float* top_p,
+                        int max_top_k, int has_top_p,
+                        float* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* race / sample (spec_sampler.py:99-111): out[r] = argmax_i weights[r,i] / noise[r,i] (first index wins ties),
+ * weights and noise fp32 [n_rows, V] with the given row strides. */
+int nvs_race(const float* weights, int64_t weights_row_stride, const float* noise, int64_t noise_row_stride,
+             int64_t n_rows, int64_t vocab, int64_t* out, void* workspace, size_t workspace_bytes, void* stream);
+int nvs_race_workspace_size(int64_t n_rows, int64_t vocab, size_t* bytes);
+
+/* accept_random_varlen (spec_sampler.py:123-150) over dense probabilities, with the generator's draws passed in:
+ * uniforms = torch.rand(B, k) and noise = exponential_noise_([B, V]) drawn in that order by the caller.
+ * p [T, V] fp32 (row stride V), q [B, k, V] fp32 contiguous, drafts [B, k] int64, verified_lens [B] int64 in
+ * 1..k+1 summing to T (NULL = every row verifies k+1 = accept_random, spec_sampler.py:114-120).
+ * Outputs n_accept [B] int64 and tail [B] int64. */
+int nvs_accept_random_workspace_size(int64_t batch, int64_t vocab, size_t* bytes);
+int nvs_accept_random(const float* p, const float* q, const int64_t* drafts, const int64_t* verified_lens,
+                      const float* uniforms, const float* noise,
+                      int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
+                      int64_t* n_accept, int64_t* tail, void* workspace, size_t workspace_bytes, void* stream);
+
+/* accept_greedy_varlen (spec_sampler.py:153-169): target tokens = argmax of each logit row (first max wins);
+ * a draft is accepted iff it equals the target token at its position; tail = the target token after the
+ * accepted prefix. verified_lens NULL = every row verifies k+1 (accept_greedy). */
+int nvs_accept_greedy_workspace_size(int64_t n_pos, int64_t vocab, size_t* bytes);
+int nvs_accept_greedy(const void* logits, int logits_dtype, int64_t logits_row_stride,
+                      const int64_t* drafts, const int64_t* verified_lens,
+                      int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
+                      int64_t* n_accept, int64_t* tail, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The fused verify sampler: probs_from_logits(logits, sampling_per_token(...)) followed by accept_random_varlen
+ * (the two calls SpeculativeDecoder._accept makes, nanovllm/engine/speculative.py:450-462), in one pass over each
+ * verified position's logit row. The [T, V] probabilities are never written: each position's kept set (top-k
+ * window plus ties, then top-p) is selected on chip, the accept test reads p and q at the draft token only, and
+ * the residual max(p - q, 0) or bonus race reads q and the noise only inside the kept set (a row with top_k = 0
+ * falls back to a full-vocabulary race). Same outputs as the two calls given the same uniforms and noise.
+ * Sampling parameters are per batch row [B] (not per token). */
+int nvs_spec_accept_workspace_size(int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab, int max_top_k,
+                                   size_t* bytes);
+int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_stride,
+                    const float* temperatures, const int64_t* top_k, const float* top_p,
+                    int max_top_k, int has_top_p,
+                    const float* q, const int64_t* drafts, const int64_t* verified_lens,
+                    const float* uniforms, const float* noise,
+                    int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
+                    int64_t* n_accept, int64_t* tail, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVS_AMD_H */

@@ -1,0 +1,86 @@
+// Shared helpers of the gfx950 kernels: status/error plumbing, dtype loads, launch checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/nvs_amd.h"
+
+namespace nvs {
+
+// Thread-local message of the last failed call, returned by nvs_last_error().
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define NVS_CHECK(cond, status, ...)          \
+    do {                                      \
+        if (!(cond)) {                        \
+            ::nvs::set_error(__VA_ARGS__);    \
+            return (status);                  \
+        }                                     \
+    } while (0)
+
+// After a kernel launch: turn a runtime launch error into NVS_ERR_HIP.
+int check_launch(const char* what);
+
+__host__ __device__ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+__host__ __device__ inline int dtype_size(int dtype) {
+    switch (dtype) {
+        case NVS_DTYPE_F32: return 4;
+        case NVS_DTYPE_BF16: return 2;
+        case NVS_DTYPE_F16: return 2;
+        default: return 0;
+    }
+}
+
+// ---------------------------------------------------------------- device helpers
+
+// bf16 / f16 bit patterns -> fp32 (exact).
+__device__ __forceinline__ float bf16_bits_to_float(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_float(uint16_t b) {
+    return __half2float(__ushort_as_half(b));
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+template <int DT>
+__device__ __forceinline__ float load_as_float(const void* base, int64_t idx) {
+    if constexpr (DT == NVS_DTYPE_F32) {
+        return static_cast<const float*>(base)[idx];
+    } else if constexpr (DT == NVS_DTYPE_BF16) {
+        return bf16_bits_to_float(static_cast<const uint16_t*>(base)[idx]);
+    } else {
+        return f16_bits_to_float(static_cast<const uint16_t*>(base)[idx]);
+    }
+}
+
+// Order-preserving map of fp32 onto uint32: a < b  <=>  key(a) < key(b) (for non-NaN; -0 < +0).
+__device__ __forceinline__ uint32_t float_key(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_float(uint32_t k) {
+    uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(u);
+}
+
+}  // namespace nvs

@@ -1,0 +1,555 @@
+// Paged multi-query verify attention for gfx950 (MI355X).
+// Reference: Attention.forward, nanovllm/layers/attention.py:59-77 (flash_attn_varlen_func with block_table in the
+// verify / cached-prefix branch, flash_attn_with_kvcache in the decode / draft-block branch); the semantics are
+// restated in tests/fake_paged_attention.py:20-41 (gather through block_tables, GQA by head group, bottom-right
+// causal rule j <= Lk - Lq + i).
+//
+// Work decomposition.
+//   One workgroup = (request row r, kv head g, query tile qt, key split s); 4 wavefronts.
+//   The query tile packs the GQA query heads of kv head g and all query positions of the row into 32 "packed rows"
+//   n = qpos * group + hg, so every K/V byte of the row's kv head is read from HBM once for all of them
+//   (Qwen3-8B: group 4 x 8 verify positions = 32 rows).
+//   The key range [0, Lk) is cut into splits of split_tokens keys; each wave of the workgroup takes every 4th
+//   32-key chunk of its split and keeps its own online-softmax state. The 4 waves are merged in LDS
+//   (deterministic order); a row with a single split writes bf16 output directly, otherwise each split writes an
+//   fp32 partial (O, max, sum) and attn_combine_kernel merges them with the log-sum-exp rule.
+//
+// Per chunk of 32 keys, per wave (lane l: packed row nl = l % 32, half gi = l / 32):
+//   S^T[32 keys x 32 rows] = K[32 x 128] . Q^T      8 x v_mfma_f32_32x32x16_bf16, K loaded straight from HBM
+//                                                    into the A-operand layout (lane = key, 8 dims per half)
+//   online softmax in fp32 with exp2 (scale * log2 e folded into one multiply); each lane owns one packed row,
+//   the two halves of a row are merged with one cross-lane exchange
+//   O^T[128 x 32] += V^T[128 x 32 keys] . P^T       8 x v_mfma_f32_32x32x16_bf16; P rounded to bf16 as the B
+//                                                    operand straight from the S accumulators; V transposed
+//                                                    through a wave-private LDS tile
+// K and V of the next chunk are loaded into registers while the current one is processed.
+#include "nvs_common.hpp"
+
+#include <cmath>
+#include <cstdlib>
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kHeadDim = 128;
+constexpr int kTileRows = 32;    // packed query rows per tile
+constexpr int kChunk = 32;       // keys per MFMA chunk
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kSplitQuantum = kChunk * kWaves;  // split_tokens is a multiple of this
+// Transposed V tile in LDS: [128 dims][32 key slots] of bf16, rows padded to 72 B so that the stores of one
+// instruction (32 keys of one dim in each half-wave, 8 dims apart) hit disjoint banks.
+constexpr int kVtStride = 36;                    // uint16 per dim row
+constexpr int kVtWaveElems = kHeadDim * kVtStride;
+constexpr int kObStride = 33;                    // fp32 per dim row of the cross-wave reduction buffer
+// Query tile in LDS: [32 packed rows][128 dims] bf16, rows padded to 272 B so the B-operand reads (32 rows at one
+// column per half-wave) spread over all banks.
+constexpr int kQsStride = kHeadDim + 8;
+
+struct AttnArgs {
+    const uint16_t* q;
+    int64_t q_ts, q_hs;
+    const uint16_t* kc;
+    const uint16_t* vc;
+    int64_t c_bs, c_ts, c_hs;
+    const int32_t* bt;
+    int64_t bt_rs;
+    int bt_width;
+    int64_t n_blocks;
+    int64_t n_tokens;
+    const int32_t* cu_q;
+    const int32_t* cu_k;
+    const int32_t* ctx;
+    int q_fixed;
+    int n_kv, group, block_size, causal;
+    float scale_log2;
+    uint16_t* out;
+    int64_t o_ts, o_hs;
+    float* part_o;   // [units, n_splits, 32, 128]
+    float* part_ml;  // [units, n_splits, 32, 2]
+    int n_splits, split_tokens, q_tiles;
+};
+
+struct RowInfo {
+    int q0, lq, lk;
+};
+
+__device__ __forceinline__ RowInfo row_info(const AttnArgs& a, int r) {
+    RowInfo ri;
+    if (a.cu_q != nullptr) {
+        ri.q0 = a.cu_q[r];
+        ri.lq = a.cu_q[r + 1] - ri.q0;
+        ri.lk = a.cu_k[r + 1] - a.cu_k[r];
+    } else {
+        ri.q0 = r * a.q_fixed;
+        ri.lq = a.q_fixed;
+        ri.lk = a.ctx[r];
+    }
+    return ri;
+}
+
+// Splits holding keys of a row with lk keys (at least one, so a row without keys still writes zeros); never more
+// than the grid has, so a length above max_seqlen_k cannot send the combine past the partial buffers.
+__device__ __forceinline__ int active_splits(int lk, int split_tokens, int n_splits) {
+    return lk > 0 ? min((lk + split_tokens - 1) / split_tokens, n_splits) : 1;
+}
+
+// Key slot inside the transposed V tile: bits 2 and 3 of the key index swapped, so the 8 keys that one lane
+// feeds to one PV MFMA (keys 16h + 4gi + {0..3} and 16h + 8 + 4gi + {0..3}) sit in 8 consecutive slots.
+__device__ __forceinline__ int vt_slot(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
+
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+__global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t vt_all[kWaves * kVtWaveElems];
+    __shared__ __attribute__((aligned(16))) uint16_t qs[kTileRows * kQsStride];
+    __shared__ float sm_m[kWaves][kTileRows];
+    __shared__ float sm_l[kWaves][kTileRows];
+
+    const int r = blockIdx.z;
+    const int g = blockIdx.y / a.q_tiles;
+    const int qt = blockIdx.y - g * a.q_tiles;
+    const int s = blockIdx.x;
+    const RowInfo ri = row_info(a, r);
+    const int n_base = qt * kTileRows;
+    if (ri.lq <= 0 || n_base >= a.group * ri.lq) return;
+    const int n_act = active_splits(ri.lk, a.split_tokens, a.n_splits);
+    if (s >= n_act) return;
+    const int k0 = s * a.split_tokens;
+    const int k1 = min(k0 + a.split_tokens, ri.lk);
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int nl = lane & 31;
+    const int gi = lane >> 5;
+
+    // The query tile -> LDS (zeros for packed rows past the row's Lq): 32 rows x 256 B, one 16 B piece per thread
+    // and pass.
+    for (int e = tid; e < kTileRows * (kHeadDim / 8); e += kThreads) {
+        const int row = e >> 4;
+        const int piece = e & 15;
+        const int nn = n_base + row;
+        const int qp = nn / a.group;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (qp < ri.lq && ri.q0 + qp < a.n_tokens && ri.q0 + qp >= 0) {
+            const int hh = g * a.group + (nn - qp * a.group);
+            v = *reinterpret_cast<const u32x4*>(a.q + static_cast<int64_t>(ri.q0 + qp) * a.q_ts +
+                                                static_cast<int64_t>(hh) * a.q_hs + 8 * piece);
+        }
+        *reinterpret_cast<u32x4*>(qs + row * kQsStride + 8 * piece) = v;
+    }
+
+    // This lane's packed query row.
+    const int n = n_base + nl;
+    const int qpos = n / a.group;
+    const int hg = n - qpos * a.group;
+    const bool qvalid = qpos < ri.lq && ri.q0 + qpos < a.n_tokens && ri.q0 + qpos >= 0;
+    const int h = g * a.group + hg;
+    // Last key this row may see inside the split (bottom-right causal alignment).
+    int lim = (a.causal && qvalid) ? (ri.lk - ri.lq + qpos) : (ri.lk - 1);
+    lim = min(lim, k1 - 1);
+
+    uint16_t* vt = vt_all + wave * kVtWaveElems;
+    const uint16_t* qrow = qs + nl * kQsStride + 8 * gi;
+    const int32_t* btr = a.bt + static_cast<int64_t>(r) * a.bt_rs;
+    const int64_t head_off = static_cast<int64_t>(g) * a.c_hs + 8 * gi;
+    const int slot = vt_slot(nl);
+
+    float m_run = -INFINITY;
+    float l_run = 0.f;
+    f32x16 o[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = f32x16{};
+
+    const int nch = (k1 - k0 + kChunk - 1) / kChunk;
+
+    // Offset of this lane's key row (clamped into [0, Lk) so a tail chunk never reads outside the row's pages;
+    // a 32-key chunk never straddles a page because block_size is a multiple of 32).
+    auto chunk_offset = [&](int c) -> int64_t {
+        const int tb = k0 + c * kChunk;
+        const int t = min(tb + nl, ri.lk - 1);
+        const int page = min(tb / a.block_size, a.bt_width - 1);
+        int64_t blk = btr[page];
+        blk = blk < 0 ? 0 : (blk >= a.n_blocks ? a.n_blocks - 1 : blk);
+        return blk * a.c_bs + static_cast<int64_t>(t - page * a.block_size) * a.c_ts + head_off;
+    };
+    auto load_k = [&](int64_t off, u32x4 (&kr)[8]) {
+        const uint16_t* kp = a.kc + off;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kr[i] = *reinterpret_cast<const u32x4*>(kp + 16 * i);
+    };
+    auto load_v = [&](int64_t off, u32x4 (&vr)[8]) {
+        const uint16_t* vp = a.vc + off;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vr[i] = *reinterpret_cast<const u32x4*>(vp + 16 * i);
+    };
+    // V rows -> transposed wave-private LDS tile. LDS executes one wave's accesses in issue order; the fences
+    // only keep the compiler from moving these stores across the previous chunk's reads.
+    auto stage_v = [&](const u32x4 (&vr)[8]) {
+        compiler_fence();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int d0 = 16 * i + 8 * gi;
+            const uint32_t w[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vt[(d0 + 2 * e) * kVtStride + slot] = static_cast<uint16_t>(w[e] & 0xffffu);
+                vt[(d0 + 2 * e + 1) * kVtStride + slot] = static_cast<uint16_t>(w[e] >> 16);
+            }
+        }
+        compiler_fence();
+    };
+
+    // One chunk: S^T = K Q^T from the K registers, then the next chunk's K and V are requested (their registers
+    // are free again), then softmax and O^T += V^T P^T from the LDS tile.
+    auto process_chunk = [&](int c, u32x4 (&kr)[8], u32x4 (&vr)[8]) {
+        const int tb = k0 + c * kChunk;
+        stage_v(vr);
+        f32x16 acc = f32x16{};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const bf16x8 qb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + 16 * i));
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kr[i]), qb, acc, 0, 0, 0);
+        }
+        const int cn = c + kWaves;
+        if (cn < nch) {
+            const int64_t off = chunk_offset(cn);
+            load_k(off, kr);
+            load_v(off, vr);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int t = tb + 8 * (j >> 2) + 4 * gi + (j & 3);
+            acc[j] = (t <= lim) ? acc[j] * a.scale_log2 : -INFINITY;
+            mx = fmaxf(mx, acc[j]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        float ps = 0.f;
+        bf16x8 pb[2];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float p = __builtin_amdgcn_exp2f(acc[j] - m_use);
+            ps += p;
+            pb[j >> 3][j & 7] = static_cast<__bf16>(p);
+        }
+        l_run = l_run * alpha + ps;
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[db] *= alpha;
+
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const uint16_t* src = vt + (32 * db + nl) * kVtStride + 16 * hh + 8 * gi;
+                const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+                const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 4);
+                const u32x4 va = {lo.x, lo.y, hi.x, hi.y};
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va), pb[hh], o[db], 0,
+                                                                0, 0);
+            }
+        }
+    };
+
+    __syncthreads();  // query tile staged
+
+    // This wave's chunks are wave, wave + 4, ...; each one's K and V are in flight while the previous is processed.
+    {
+        u32x4 kr[8], vr[8];
+        if (wave < nch) {
+            const int64_t off = chunk_offset(wave);
+            load_k(off, kr);
+            load_v(off, vr);
+        }
+        for (int c = wave; c < nch; c += kWaves) process_chunk(c, kr, vr);
+    }
+
+    // ---- merge the 4 waves (fixed order, so the result does not depend on timing)
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    if (gi == 0) {
+        sm_m[wave][nl] = m_run;
+        sm_l[wave][nl] = l_tot;
+    }
+    __syncthreads();
+    float mw[kWaves];
+    float m_all = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        mw[w] = sm_m[w][nl];
+        m_all = fmaxf(m_all, mw[w]);
+    }
+    const float m_all_use = (m_all == -INFINITY) ? 0.f : m_all;
+    float l_all = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) l_all += sm_l[w][nl] * __builtin_amdgcn_exp2f(mw[w] - m_all_use);
+    const float own = __builtin_amdgcn_exp2f(m_run - m_all_use);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] *= own;
+
+    float* ob = reinterpret_cast<float*>(vt_all);  // the V tiles are dead after the barrier above
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        if (wave == w) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int d = 32 * db + 8 * (j >> 2) + 4 * gi + (j & 3);
+                    float v = o[db][j];
+                    if (w > 0) v += ob[d * kObStride + nl];
+                    o[db][j] = v;
+                    if (w < kWaves - 1) ob[d * kObStride + nl] = v;
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (wave != kWaves - 1 || !qvalid) return;
+
+    if (n_act == 1) {
+        const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
+        uint16_t* op = a.out + static_cast<int64_t>(ri.q0 + qpos) * a.o_ts + static_cast<int64_t>(h) * a.o_hs;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {
+                const int d = 32 * db + 8 * jq + 4 * gi;
+                const uint32_t lo = nvs::float_to_bf16_bits(o[db][4 * jq + 0] * inv) |
+                                    (static_cast<uint32_t>(nvs::float_to_bf16_bits(o[db][4 * jq + 1] * inv)) << 16);
+                const uint32_t hi = nvs::float_to_bf16_bits(o[db][4 * jq + 2] * inv) |
+                                    (static_cast<uint32_t>(nvs::float_to_bf16_bits(o[db][4 * jq + 3] * inv)) << 16);
+                *reinterpret_cast<u32x2*>(op + d) = u32x2{lo, hi};
+            }
+        }
+    } else {
+        const int64_t unit = (static_cast<int64_t>(r) * a.n_kv + g) * a.q_tiles + qt;
+        const int64_t pidx = unit * a.n_splits + s;
+        float* po = a.part_o + (pidx * kTileRows + nl) * kHeadDim;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {
+                const int d = 32 * db + 8 * jq + 4 * gi;
+                *reinterpret_cast<float4*>(po + d) =
+                    make_float4(o[db][4 * jq], o[db][4 * jq + 1], o[db][4 * jq + 2], o[db][4 * jq + 3]);
+            }
+        }
+        if (gi == 0) {
+            float* pm = a.part_ml + (pidx * kTileRows + nl) * 2;
+            pm[0] = m_all;
+            pm[1] = l_all;
+        }
+    }
+}
+
+// Merge the split partials of every (row, kv head, query tile) that had more than one active split.
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+    const int r = blockIdx.y;
+    const int g = blockIdx.x / a.q_tiles;
+    const int qt = blockIdx.x - g * a.q_tiles;
+    const RowInfo ri = row_info(a, r);
+    const int n_base = qt * kTileRows;
+    if (ri.lq <= 0 || n_base >= a.group * ri.lq) return;
+    const int n_act = active_splits(ri.lk, a.split_tokens, a.n_splits);
+    if (n_act <= 1) return;
+    const int64_t unit = (static_cast<int64_t>(r) * a.n_kv + g) * a.q_tiles + qt;
+    for (int e = threadIdx.x; e < kTileRows * kHeadDim / 4; e += blockDim.x) {
+        const int nl = e / (kHeadDim / 4);
+        const int d = (e - nl * (kHeadDim / 4)) * 4;
+        const int n = n_base + nl;
+        const int qpos = n / a.group;
+        if (qpos >= ri.lq || ri.q0 + qpos >= a.n_tokens || ri.q0 + qpos < 0) continue;
+        const int h = g * a.group + (n - qpos * a.group);
+        float m_all = -INFINITY;
+        for (int s = 0; s < n_act; ++s) m_all = fmaxf(m_all, a.part_ml[((unit * a.n_splits + s) * kTileRows + nl) * 2]);
+        const float m_use = (m_all == -INFINITY) ? 0.f : m_all;
+        float l_all = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s = 0; s < n_act; ++s) {
+            const int64_t pidx = (unit * a.n_splits + s) * kTileRows + nl;
+            const float w = __builtin_amdgcn_exp2f(a.part_ml[pidx * 2] - m_use);
+            l_all += a.part_ml[pidx * 2 + 1] * w;
+            const float4 v = *reinterpret_cast<const float4*>(a.part_o + pidx * kHeadDim + d);
+            acc.x += v.x * w;
+            acc.y += v.y * w;
+            acc.z += v.z * w;
+            acc.w += v.w * w;
+        }
+        const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
+        uint16_t* op = a.out + static_cast<int64_t>(ri.q0 + qpos) * a.o_ts + static_cast<int64_t>(h) * a.o_hs + d;
+        const uint32_t lo = nvs::float_to_bf16_bits(acc.x * inv) |
+                            (static_cast<uint32_t>(nvs::float_to_bf16_bits(acc.y * inv)) << 16);
+        const uint32_t hi = nvs::float_to_bf16_bits(acc.z * inv) |
+                            (static_cast<uint32_t>(nvs::float_to_bf16_bits(acc.w * inv)) << 16);
+        *reinterpret_cast<u32x2*>(op) = u32x2{lo, hi};
+    }
+}
+
+struct SplitPlan {
+    int q_tiles, n_splits, split_tokens;
+    size_t workspace;
+};
+
+// Key-split plan: enough workgroups to fill the 256 CUs a few times over, each wave still streaming several
+// chunks. Depends only on host integers, so it is stable under graph capture.
+SplitPlan plan_splits(int n_rows, int n_heads, int n_kv_heads, int max_seqlen_q, int max_seqlen_k) {
+    SplitPlan p;
+    const int group = n_heads / n_kv_heads;
+    p.q_tiles = (group * max_seqlen_q + kTileRows - 1) / kTileRows;
+    const int64_t units = static_cast<int64_t>(n_rows) * n_kv_heads * p.q_tiles;
+    int64_t target = 1024;
+    if (const char* env = std::getenv("NVS_ATTN_TARGET_WGS")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v > 0) target = v;
+    }
+    int64_t want = units > 0 ? (target + units - 1) / units : 1;
+    if (want < 1) want = 1;
+    const int64_t max_k = max_seqlen_k > 0 ? max_seqlen_k : 1;
+    int64_t ts = (max_k + want - 1) / want;
+    int64_t min_ts = 2 * kSplitQuantum;
+    if (const char* env = std::getenv("NVS_ATTN_MIN_SPLIT")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v > 0) min_ts = v;
+    }
+    ts = (ts + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum;
+    min_ts = (min_ts + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum;
+    if (ts < min_ts) ts = min_ts;
+    p.split_tokens = static_cast<int>(ts);
+    p.n_splits = static_cast<int>((max_k + ts - 1) / ts);
+    if (p.n_splits < 1) p.n_splits = 1;
+    p.workspace = 0;
+    if (p.n_splits > 1) {
+        const size_t per = static_cast<size_t>(kTileRows) * (kHeadDim + 2) * sizeof(float);
+        p.workspace = static_cast<size_t>(units) * p.n_splits * per + 256;
+    }
+    return p;
+}
+
+int validate_sizes(int n_rows, int n_heads, int n_kv_heads, int head_dim, int max_seqlen_q, int max_seqlen_k) {
+    NVS_CHECK(n_rows >= 0 && max_seqlen_q >= 0 && max_seqlen_k >= 0, NVS_ERR_INVALID,
+              "paged_attention: negative size (n_rows=%d max_seqlen_q=%d max_seqlen_k=%d)", n_rows, max_seqlen_q,
+              max_seqlen_k);
+    NVS_CHECK(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, NVS_ERR_INVALID,
+              "paged_attention: n_heads=%d must be a positive multiple of n_kv_heads=%d", n_heads, n_kv_heads);
+    NVS_CHECK(head_dim == kHeadDim, NVS_ERR_UNSUPPORTED, "paged_attention: head_dim %d unsupported (only 128)",
+              head_dim);
+    return NVS_OK;
+}
+
+}  // namespace
+
+extern "C" int nvs_paged_attention_workspace_size(int n_rows, int n_heads, int n_kv_heads, int head_dim,
+                                                  int max_seqlen_q, int max_seqlen_k, size_t* bytes) {
+    nvs::clear_error();
+    NVS_CHECK(bytes != nullptr, NVS_ERR_INVALID, "paged_attention_workspace_size: bytes is NULL");
+    const int st = validate_sizes(n_rows, n_heads, n_kv_heads, head_dim, max_seqlen_q, max_seqlen_k);
+    if (st != NVS_OK) return st;
+    *bytes = plan_splits(n_rows, n_heads, n_kv_heads, max_seqlen_q, max_seqlen_k).workspace;
+    return NVS_OK;
+}
+
+extern "C" int nvs_paged_attention(const void* q, int64_t q_token_stride, int64_t q_head_stride, int64_t n_tokens,
+                                   const void* k_cache, const void* v_cache, int64_t cache_blocks,
+                                   int64_t cache_block_stride, int64_t cache_token_stride,
+                                   int64_t cache_head_stride, const int32_t* block_tables, int64_t bt_row_stride,
+                                   int bt_width, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                   const int32_t* context_lens, int query_len_per_seq, int n_rows, int max_seqlen_q,
+                                   int max_seqlen_k, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                                   float scale, int causal, int dtype, void* out, int64_t out_token_stride,
+                                   int64_t out_head_stride, void* workspace, size_t workspace_bytes, void* stream) {
+    nvs::clear_error();
+    int st = validate_sizes(n_rows, n_heads, n_kv_heads, head_dim, max_seqlen_q, max_seqlen_k);
+    if (st != NVS_OK) return st;
+    NVS_CHECK(dtype == NVS_DTYPE_BF16, NVS_ERR_UNSUPPORTED, "paged_attention: dtype %d unsupported (only bf16)",
+              dtype);
+    const bool varlen = cu_seqlens_q != nullptr || cu_seqlens_k != nullptr;
+    NVS_CHECK(!varlen || (cu_seqlens_q != nullptr && cu_seqlens_k != nullptr), NVS_ERR_INVALID,
+              "paged_attention: cu_seqlens_q and cu_seqlens_k must both be given (varlen) or both NULL");
+    NVS_CHECK(varlen || context_lens != nullptr, NVS_ERR_INVALID,
+              "paged_attention: fixed mode needs context_lens");
+    NVS_CHECK(varlen || query_len_per_seq >= 1, NVS_ERR_INVALID,
+              "paged_attention: query_len_per_seq must be >= 1, got %d", query_len_per_seq);
+    NVS_CHECK(varlen || query_len_per_seq <= max_seqlen_q, NVS_ERR_INVALID,
+              "paged_attention: query_len_per_seq %d exceeds max_seqlen_q %d", query_len_per_seq, max_seqlen_q);
+    NVS_CHECK(block_size > 0 && block_size % kChunk == 0, NVS_ERR_UNSUPPORTED,
+              "paged_attention: block_size %d must be a positive multiple of %d", block_size, kChunk);
+    if (n_rows == 0 || max_seqlen_q == 0 || n_tokens == 0) return NVS_OK;
+    NVS_CHECK(n_tokens > 0 && cache_blocks > 0 && bt_width > 0, NVS_ERR_INVALID,
+              "paged_attention: n_tokens=%lld, cache_blocks=%lld and bt_width=%d must be positive",
+              (long long)n_tokens, (long long)cache_blocks, bt_width);
+    NVS_CHECK(q && k_cache && v_cache && block_tables && out, NVS_ERR_INVALID, "paged_attention: null pointer");
+    NVS_CHECK(nvs::aligned16(q) && nvs::aligned16(k_cache) && nvs::aligned16(v_cache), NVS_ERR_INVALID,
+              "paged_attention: q, k_cache and v_cache must be 16-byte aligned");
+    NVS_CHECK(q_token_stride % 8 == 0 && q_head_stride % 8 == 0 && cache_block_stride % 8 == 0 &&
+                  cache_token_stride % 8 == 0 && cache_head_stride % 8 == 0,
+              NVS_ERR_INVALID, "paged_attention: q and cache strides must be multiples of 8 elements");
+    NVS_CHECK((reinterpret_cast<uintptr_t>(out) & 7u) == 0 && out_token_stride % 4 == 0 && out_head_stride % 4 == 0,
+              NVS_ERR_INVALID, "paged_attention: out must be 8-byte aligned with strides multiple of 4");
+    NVS_CHECK(scale > 0.f && std::isfinite(scale), NVS_ERR_INVALID, "paged_attention: bad scale %g", (double)scale);
+
+    const SplitPlan plan = plan_splits(n_rows, n_heads, n_kv_heads, max_seqlen_q, max_seqlen_k);
+    NVS_CHECK(plan.workspace == 0 || (workspace != nullptr && workspace_bytes >= plan.workspace),
+              NVS_ERR_WORKSPACE, "paged_attention: workspace of %zu bytes needed, %zu given", plan.workspace,
+              workspace_bytes);
+    NVS_CHECK(static_cast<int64_t>(n_kv_heads) * plan.q_tiles <= 65535 && n_rows <= 65535, NVS_ERR_UNSUPPORTED,
+              "paged_attention: grid too large (rows %d, kv heads x tiles %lld)", n_rows,
+              (long long)n_kv_heads * plan.q_tiles);
+
+    AttnArgs a;
+    a.q = static_cast<const uint16_t*>(q);
+    a.q_ts = q_token_stride;
+    a.q_hs = q_head_stride;
+    a.kc = static_cast<const uint16_t*>(k_cache);
+    a.vc = static_cast<const uint16_t*>(v_cache);
+    a.c_bs = cache_block_stride;
+    a.c_ts = cache_token_stride;
+    a.c_hs = cache_head_stride;
+    a.bt = block_tables;
+    a.bt_rs = bt_row_stride;
+    a.bt_width = bt_width;
+    a.n_blocks = cache_blocks;
+    a.n_tokens = n_tokens;
+    a.cu_q = varlen ? cu_seqlens_q : nullptr;
+    a.cu_k = varlen ? cu_seqlens_k : nullptr;
+    a.ctx = varlen ? nullptr : context_lens;
+    a.q_fixed = varlen ? 0 : query_len_per_seq;
+    a.n_kv = n_kv_heads;
+    a.group = n_heads / n_kv_heads;
+    a.block_size = block_size;
+    a.causal = causal ? 1 : 0;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.out = static_cast<uint16_t*>(out);
+    a.o_ts = out_token_stride;
+    a.o_hs = out_head_stride;
+    char* ws = static_cast<char*>(workspace);
+    const size_t po_bytes = plan.n_splits > 1 ? nvs::align_up(static_cast<size_t>(n_rows) * n_kv_heads *
+                                                                   plan.q_tiles * plan.n_splits * kTileRows *
+                                                                   kHeadDim * sizeof(float),
+                                                               256)
+                                              : 0;
+    a.part_o = plan.n_splits > 1 ? reinterpret_cast<float*>(ws) : nullptr;
+    a.part_ml = plan.n_splits > 1 ? reinterpret_cast<float*>(ws + po_bytes) : nullptr;
+    a.n_splits = plan.n_splits;
+    a.split_tokens = plan.split_tokens;
+    a.q_tiles = plan.q_tiles;
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid(plan.n_splits, n_kv_heads * plan.q_tiles, n_rows);
+    hipLaunchKernelGGL(attn_split_kernel, grid, dim3(kThreads), 0, s, a);
+    st = nvs::check_launch("paged_attention split kernel");
+    if (st != NVS_OK) return st;
+    if (plan.n_splits > 1) {
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(n_kv_heads * plan.q_tiles, n_rows), dim3(256), 0, s, a);
+        st = nvs::check_launch("paged_attention combine kernel");
+    }
+    return st;
+}

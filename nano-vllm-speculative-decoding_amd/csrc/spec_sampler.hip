@@ -1,0 +1,1378 @@
+// Speculative sampler for gfx950: truncation -> softmax -> rejection test -> residual / bonus race.
+// Reference: nanovllm/layers/spec_sampler.py (probs_from_logits :65-69, truncate_logits :72-96, race / sample
+// :99-111, accept_random(_varlen) :114-150, accept_greedy(_varlen) :153-169, _verified_positions :172-180) as
+// dispatched by SpeculativeDecoder._accept, nanovllm/engine/speculative.py:450-462.
+//
+// Selection kernel (one 512-thread workgroup per logit row = verify position):
+//   * one coalesced pass over the row: s = logit / temperature (IEEE division, skipped when it is exactly 1);
+//   * rows that truncate (top_k > 0): every element at or above a running lower bound tau of the row's
+//     max_top_k-th largest value is appended to an LDS candidate list. tau starts from the first 8192 elements:
+//     each wave takes the ceil(K/8)-th largest of its 64 lane maxima, tau is the smallest of the 8, so at least K
+//     elements lie at or above it. When the list passes half its capacity it is pruned to its exact K-th largest.
+//     The list therefore holds every element >= the K-th largest, ties included, and nothing else is needed;
+//   * exact radix select (8-bit digits over the order-preserving key of each float) in LDS gives the row's
+//     rank-th largest value (rank = min(top_k, K)); top-p sorts the candidates above it (bitonic, LDS) and runs
+//     the nucleus softmax / cumsum of truncate_logits; the kept set is {s >= threshold} (ties kept);
+//   * rows that do not truncate (top_k = 0) keep an online max / sum-exp instead;
+//   * a list that overflows (thousands of tied values) falls back to an exact radix select over the row itself.
+// Then, depending on the entry point: write dense probabilities (probs_from_logits), write truncated logits
+// (truncate_logits), or (fused accept) evaluate this position's accept test u * q[d] < p[d] and its race:
+// argmax over the kept set of w / E with w = p (bonus position) or max(p - q, 0) (first rejection here), reading
+// q and E only at the kept indices. A finalize kernel per batch row counts the accepted prefix and picks the race
+// of the position that follows it (or races over the whole vocabulary for rows that do not truncate).
+#include "nvs_common.hpp"
+
+#include <cmath>
+
+namespace {
+
+constexpr int kSelThreads = 512;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kVpt = 16;                       // values per thread per batch
+constexpr int kBatch = kSelThreads * kVpt;     // 8192 elements per batch
+constexpr int kCap = 4096;                     // LDS candidate capacity
+constexpr int kMaxTopK = 1024;
+constexpr int kRaceChunk = 16384;              // vocabulary chunk of the dense race kernels
+
+enum Mode { kModeAccept = 0, kModeProbs = 1, kModeTruncate = 2 };
+
+constexpr int kFlagDense = 1;  // the race of this position must scan the whole vocabulary
+
+struct PosRecord {
+    float m;        // max of the kept set
+    float z;        // sum of exp(s - m) over the kept set
+    float theta;    // truncation threshold (-inf when nothing is truncated)
+    float temp;     // temperature of the row
+    int flags;
+    int acc;        // accept decision of the draft verified at this position
+    int64_t race;   // winner of this position's race (valid unless kFlagDense)
+};
+static_assert(sizeof(PosRecord) == 32, "record layout");
+
+struct SelArgs {
+    const void* logits;
+    int64_t row_stride;
+    int64_t n_pos;
+    int64_t vocab;
+    const float* temps;
+    const int64_t* top_k;
+    const float* top_p;
+    int max_top_k;
+    int has_top_p;
+    int64_t pos_per_param;
+    // fused accept
+    const float* q;
+    const int64_t* drafts;
+    const int64_t* lens;
+    const float* uniforms;
+    const float* noise;
+    int64_t batch;
+    int k;
+    PosRecord* rec;
+    // dense outputs
+    float* out;
+    int64_t out_stride;
+};
+
+// ---------------------------------------------------------------- wave / workgroup helpers
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), o)));
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t w = __shfl_xor(v, o);
+        v = v > w ? v : w;
+    }
+    return v;
+}
+
+// Inclusive prefix sum over the wave.
+__device__ __forceinline__ float wave_scan_incl(float v) {
+    const int l = lane_id();
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float w = __shfl_up(v, o);
+        if (l >= o) v += w;
+    }
+    return v;
+}
+
+__device__ __forceinline__ int64_t wave_scan_incl_i64(int64_t v) {
+    const int l = lane_id();
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int64_t w = __shfl_up(v, o);
+        if (l >= o) v += w;
+    }
+    return v;
+}
+
+// Descending bitonic sort of one value per lane across the wave; returns this lane's sorted value.
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v) {
+    const int l = lane_id();
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const uint32_t w = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), stride));
+            const bool desc_block = ((l & size) == 0);
+            const bool lower = ((l & stride) == 0);
+            // In a descending block the lower lane keeps the larger value.
+            const bool keep_max = (lower == desc_block);
+            v = keep_max ? max(v, w) : min(v, w);
+        }
+    }
+    return v;
+}
+
+struct SelShared {
+    uint32_t ckey[kCap];
+    int32_t cidx[kCap];
+    uint32_t hist[256];
+    uint32_t sortbuf[kMaxTopK];
+    float fred[kSelWaves];
+    uint32_t ured[kSelWaves];
+    uint64_t u64red[kSelWaves];
+    int count;
+    int overflow;
+    uint32_t sel_digit, sel_remaining, sel_greater, sel_equal;
+    int64_t loc[4];  // b, j, L, start
+};
+
+// Sum over the workgroup (every thread gets the result).
+__device__ float block_sum(float v, SelShared& sh) {
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane_id() == 0) sh.fred[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int w = 0; w < kSelWaves; ++w) t += sh.fred[w];
+    return t;
+}
+
+__device__ uint32_t block_max_u32(uint32_t v, SelShared& sh) {
+    v = wave_max_u32(v);
+    __syncthreads();
+    if (lane_id() == 0) sh.ured[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint32_t t = 0;
+    for (int w = 0; w < kSelWaves; ++w) t = max(t, sh.ured[w]);
+    return t;
+}
+
+__device__ uint64_t block_max_u64(uint64_t v, SelShared& sh) {
+    v = wave_max_u64(v);
+    __syncthreads();
+    if (lane_id() == 0) sh.u64red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint64_t t = 0;
+    for (int w = 0; w < kSelWaves; ++w) t = sh.u64red[w] > t ? sh.u64red[w] : t;
+    return t;
+}
+
+// One radix-select pass: after every key of the current prefix has been counted into sh.hist, wave 0 picks the
+// digit holding the remaining-th largest key. Returns nothing; updates sh.sel_* (read after the barrier).
+__device__ void radix_pick_digit(SelShared& sh) {
+    if ((threadIdx.x >> 6) == 0) {
+        const int l = lane_id();
+        // lane l holds bins 4l .. 4l+3
+        uint32_t h[4];
+        uint32_t tot = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h[i] = sh.hist[4 * l + i];
+            tot += h[i];
+        }
+        // exclusive suffix sum over lanes: counts in bins of higher lanes
+        uint32_t suf = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t w = static_cast<uint32_t>(__shfl_down(static_cast<int>(suf), o));
+            if (l + o < 64) suf += w;
+        }
+        uint32_t above = suf - tot;  // keys in bins of lanes > l
+        const uint32_t rem = sh.sel_remaining;
+#pragma unroll
+        for (int i = 3; i >= 0; --i) {
+            if (above < rem && rem <= above + h[i]) {
+                sh.sel_digit = static_cast<uint32_t>(4 * l + i);
+                sh.sel_remaining = rem - above;
+                sh.sel_greater += above;
+                sh.sel_equal = h[i];
+            }
+            above += h[i];
+        }
+    }
+}
+
+// rank-th largest key (1-based) among the keys produced by for_each(fn) (each thread visits its share and calls
+// fn(key)). Also returns how many keys are greater / equal. Every thread gets the results.
+template <class ForEach>
+__device__ uint32_t radix_select(ForEach for_each, uint32_t rank, SelShared& sh, uint32_t* n_greater,
+                                 uint32_t* n_equal) {
+    uint32_t prefix = 0, mask = 0;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        sh.sel_remaining = rank;
+        sh.sel_greater = 0;
+        sh.sel_equal = 0;
+        sh.sel_digit = 0;
+    }
+#pragma unroll 1
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) sh.hist[i] = 0;
+        __syncthreads();
+        for_each([&](uint32_t key) {
+            if ((key & mask) == prefix) atomicAdd(&sh.hist[(key >> shift) & 255u], 1u);
+        });
+        __syncthreads();
+        radix_pick_digit(sh);
+        __syncthreads();
+        prefix |= sh.sel_digit << shift;
+        mask |= 255u << shift;
+    }
+    *n_greater = sh.sel_greater;
+    *n_equal = sh.sel_equal;
+    return prefix;
+}
+
+// Descending bitonic sort of sh.sortbuf[0..n) (n <= kMaxTopK), padding with 0 keys.
+__device__ void block_sort_desc(SelShared& sh, int n) {
+    int p = 64;
+    while (p < n) p <<= 1;
+    for (int i = n + threadIdx.x; i < p; i += blockDim.x) sh.sortbuf[i] = 0u;
+    __syncthreads();
+    for (int size = 2; size <= p; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < p / 2; i += blockDim.x) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const uint32_t a = sh.sortbuf[lo], b = sh.sortbuf[hi];
+                const bool desc = ((lo & size) == 0);
+                if (desc ? (a < b) : (a > b)) {
+                    sh.sortbuf[lo] = b;
+                    sh.sortbuf[hi] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Row locator of the fused accept: position t -> batch row b, draft index j, verified length L, first position.
+__device__ void locate(const SelArgs& a, int64_t t, SelShared& sh) {
+    if (a.lens == nullptr) {
+        if (threadIdx.x == 0) {
+            const int64_t L = a.k + 1;
+            sh.loc[0] = t / L;
+            sh.loc[1] = t % L;
+            sh.loc[2] = L;
+            sh.loc[3] = (t / L) * L;
+        }
+        __syncthreads();
+        return;
+    }
+    int64_t carry = 0;
+    for (int64_t base = 0; base < a.batch; base += blockDim.x) {
+        const int64_t i = base + threadIdx.x;
+        const int64_t L = i < a.batch ? a.lens[i] : 0;
+        int64_t incl = wave_scan_incl_i64(L);
+        // wave totals -> exclusive offsets
+        __shared__ int64_t wtot[kSelWaves];
+        if (lane_id() == 63) wtot[threadIdx.x >> 6] = incl;
+        __syncthreads();
+        int64_t off = carry;
+        for (int w = 0; w < (int)(threadIdx.x >> 6); ++w) off += wtot[w];
+        int64_t total = 0;
+        for (int w = 0; w < kSelWaves; ++w) total += wtot[w];
+        incl += off;
+        const int64_t start = incl - L;
+        __syncthreads();
+        if (i < a.batch && L > 0 && t >= start && t < incl) {
+            sh.loc[0] = i;
+            sh.loc[1] = t - start;
+            sh.loc[2] = L;
+            sh.loc[3] = start;
+        }
+        carry += total;
+    }
+    __syncthreads();
+}
+
+template <int DT>
+__device__ __forceinline__ void load_vals(const void* row, int64_t e0, int64_t vocab, bool vec, float (&v)[kVpt]) {
+    // elements e0 + 4*(i*kSelThreads) + ... : each thread handles kVpt values per batch in 16-byte pieces
+    if constexpr (DT == NVS_DTYPE_F32) {
+        const float* p = static_cast<const float*>(row);
+#pragma unroll
+        for (int i = 0; i < kVpt / 4; ++i) {
+            const int64_t e = e0 + (static_cast<int64_t>(i) * kSelThreads + threadIdx.x) * 4;
+            if (vec && e + 4 <= vocab) {
+                const float4 x = *reinterpret_cast<const float4*>(p + e);
+                v[4 * i] = x.x;
+                v[4 * i + 1] = x.y;
+                v[4 * i + 2] = x.z;
+                v[4 * i + 3] = x.w;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[4 * i + c] = (e + c < vocab) ? p[e + c] : NAN;
+            }
+        }
+    } else {
+        const uint16_t* p = static_cast<const uint16_t*>(row);
+#pragma unroll
+        for (int i = 0; i < kVpt / 8; ++i) {
+            const int64_t e = e0 + (static_cast<int64_t>(i) * kSelThreads + threadIdx.x) * 8;
+            if (vec && e + 8 <= vocab) {
+                const uint4 x = *reinterpret_cast<const uint4*>(p + e);
+                const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if constexpr (DT == NVS_DTYPE_BF16) {
+                        v[8 * i + 2 * c] = nvs::bf16_bits_to_float(static_cast<uint16_t>(w[c] & 0xffffu));
+                        v[8 * i + 2 * c + 1] = nvs::bf16_bits_to_float(static_cast<uint16_t>(w[c] >> 16));
+                    } else {
+                        v[8 * i + 2 * c] = nvs::f16_bits_to_float(static_cast<uint16_t>(w[c] & 0xffffu));
+                        v[8 * i + 2 * c + 1] = nvs::f16_bits_to_float(static_cast<uint16_t>(w[c] >> 16));
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < 8; ++c) v[8 * i + c] = (e + c < vocab) ? nvs::load_as_float<DT>(row, e + c) : NAN;
+            }
+        }
+    }
+}
+
+// Element index of value slot vi of this thread within the batch starting at e0.
+template <int DT>
+__device__ __forceinline__ int64_t val_index(int64_t e0, int vi) {
+    if constexpr (DT == NVS_DTYPE_F32) {
+        return e0 + (static_cast<int64_t>(vi >> 2) * kSelThreads + threadIdx.x) * 4 + (vi & 3);
+    } else {
+        return e0 + (static_cast<int64_t>(vi >> 3) * kSelThreads + threadIdx.x) * 8 + (vi & 7);
+    }
+}
+
+__device__ __forceinline__ float scale_logit(float x, float temp, bool unit_temp) {
+    return unit_temp ? x : x / temp;
+}
+
+// Key of a value for selection; NaN padding (past the vocabulary) maps to 0, below every real value.
+__device__ __forceinline__ uint32_t sel_key(float s) { return (s != s) ? 0u : nvs::float_key(s); }
+
+// Append the values of this thread with key >= tau_key to the candidate list.
+template <int DT>
+__device__ __forceinline__ void append_candidates(SelShared& sh, const uint32_t (&keys)[kVpt], int64_t e0,
+                                                  uint32_t tau_key) {
+    uint64_t bal[kVpt];
+    int tot = 0;
+#pragma unroll
+    for (int vi = 0; vi < kVpt; ++vi) {
+        const bool pass = keys[vi] != 0u && keys[vi] >= tau_key;
+        bal[vi] = __ballot(pass);
+        tot += __popcll(bal[vi]);
+    }
+    if (tot == 0) return;
+    int base = 0;
+    if (lane_id() == 0) base = atomicAdd(&sh.count, tot);
+    base = __shfl(base, 0);
+    const uint64_t below = (lane_id() == 0) ? 0ull : (~0ull >> (64 - lane_id()));
+    int run = 0;
+#pragma unroll
+    for (int vi = 0; vi < kVpt; ++vi) {
+        if ((bal[vi] >> lane_id()) & 1ull) {
+            const int pos = base + run + __popcll(bal[vi] & below);
+            if (pos < kCap) {
+                sh.ckey[pos] = keys[vi];
+                sh.cidx[pos] = static_cast<int32_t>(val_index<DT>(e0, vi));
+            } else {
+                sh.overflow = 1;
+            }
+        }
+        run += __popcll(bal[vi]);
+    }
+}
+
+// Keep only candidates with key >= tau_key (order not preserved). Count must be <= kCap.
+__device__ void compact_candidates(SelShared& sh, uint32_t tau_key) {
+    constexpr int kPer = kCap / kSelThreads;
+    uint32_t k[kPer];
+    int32_t ix[kPer];
+    const int n = min(sh.count, kCap);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int c = threadIdx.x + i * kSelThreads;
+        k[i] = c < n ? sh.ckey[c] : 0u;
+        ix[i] = c < n ? sh.cidx[c] : 0;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) sh.count = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const bool keep = k[i] != 0u && k[i] >= tau_key;
+        const uint64_t bal = __ballot(keep);
+        const int cnt = __popcll(bal);
+        if (cnt == 0) continue;
+        int base = 0;
+        if (lane_id() == 0) base = atomicAdd(&sh.count, cnt);
+        base = __shfl(base, 0);
+        const uint64_t below = (lane_id() == 0) ? 0ull : (~0ull >> (64 - lane_id()));
+        if (keep) {
+            const int pos = base + __popcll(bal & below);
+            sh.ckey[pos] = k[i];
+            sh.cidx[pos] = ix[i];
+        }
+    }
+    __syncthreads();
+}
+
+// Threshold of truncate_logits (spec_sampler.py:72-96) from the sorted top `rank` keys in sh.sortbuf:
+// rank = min(max(top_k, 1), K); ranks >= rank are -inf among the K candidates; with top-p the nucleus softmax
+// over the candidates, mass_before = cumsum - nucleus, kept = #(mass_before < top_p), p_threshold =
+// candidates[kept - 1]. Returns max(candidates[rank-1], p_threshold).
+__device__ float top_p_threshold(SelShared& sh, int rank, int K, float top_p, float thr) {
+    __shared__ float result;
+    if ((threadIdx.x >> 6) == 0) {
+        const int l = lane_id();
+        const float m = nvs::key_float(sh.sortbuf[0]);
+        const int per = (rank + 63) / 64;
+        float e[16];
+        float lsum = 0.f;
+        for (int i = 0; i < per && i < 16; ++i) {
+            const int r = l * per + i;
+            e[i] = (r < rank) ? expf(nvs::key_float(sh.sortbuf[r]) - m) : 0.f;
+            lsum += e[i];
+        }
+        const float total = wave_sum(lsum);
+        // local cumsum of nucleus values, then the lanes' exclusive prefix
+        float loc = 0.f;
+        for (int i = 0; i < per && i < 16; ++i) {
+            e[i] = e[i] / total;
+            loc += e[i];
+        }
+        const float incl = wave_scan_incl(loc);
+        float run = incl - loc;
+        int kept = 0;
+        for (int i = 0; i < per && i < 16; ++i) {
+            const int r = l * per + i;
+            if (r < rank) {
+                run += e[i];
+                const float before = run - e[i];
+                kept += (before < top_p) ? 1 : 0;
+            }
+        }
+        float last_cum = __shfl(incl, 63);  // cumsum at rank - 1 (all later entries add zero)
+        int kept_all = static_cast<int>(wave_sum(static_cast<float>(kept)));
+        if (last_cum < top_p) kept_all += K - rank;
+        if (l == 0) {
+            float p_thr = -INFINITY;
+            if (kept_all >= 1 && kept_all - 1 < rank) p_thr = nvs::key_float(sh.sortbuf[kept_all - 1]);
+            result = fmaxf(thr, p_thr);
+        }
+    }
+    __syncthreads();
+    return result;
+}
+
+struct RowStats {
+    float m, z, theta;
+    bool dense;   // kept set not held in the candidate list
+};
+
+// Full-row exact path (candidate list overflowed): radix select on the row, then rebuild the candidate list.
+template <int DT>
+__device__ RowStats exact_row_stats(const SelArgs& a, const void* row, bool vec, float temp, bool unit_temp,
+                                    int rank, int K, float top_p, SelShared& sh) {
+    auto for_each = [&](auto&& fn) {
+        for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
+            float v[kVpt];
+            load_vals<DT>(row, e0, a.vocab, vec, v);
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) {
+                const uint32_t key = sel_key(scale_logit(v[vi], temp, unit_temp));
+                if (key != 0u) fn(key);
+            }
+        }
+    };
+    uint32_t n_gt = 0, n_eq = 0;
+    const uint32_t thr_key = radix_select(for_each, static_cast<uint32_t>(rank), sh, &n_gt, &n_eq);
+    const bool fits = (n_gt + n_eq) <= static_cast<uint32_t>(kCap);
+    // Rebuild the candidate list: everything >= thr when it fits, else only the (fewer than rank) keys above it.
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        sh.count = 0;
+        sh.overflow = 0;
+    }
+    __syncthreads();
+    const uint32_t floor_key = fits ? thr_key : thr_key + 1u;
+    for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
+        float v[kVpt];
+        load_vals<DT>(row, e0, a.vocab, vec, v);
+        uint32_t keys[kVpt];
+#pragma unroll
+        for (int vi = 0; vi < kVpt; ++vi) keys[vi] = sel_key(scale_logit(v[vi], temp, unit_temp));
+        append_candidates<DT>(sh, keys, e0, floor_key);
+    }
+    __syncthreads();
+    RowStats rs;
+    const int n = min(sh.count, kCap);
+    // max
+    uint32_t mk = 0;
+    for (int c = threadIdx.x; c < n; c += blockDim.x) mk = max(mk, sh.ckey[c]);
+    mk = block_max_u32(mk, sh);
+    if (n == 0) mk = thr_key;
+    rs.m = nvs::key_float(mk);
+    const float thr = nvs::key_float(thr_key);
+    rs.theta = thr;
+    if (a.has_top_p) {
+        // sorted top rank keys: the ones above thr, then copies of thr
+        // gather keys > thr into sortbuf
+        __shared__ int gcount;
+        if (threadIdx.x == 0) gcount = 0;
+        __syncthreads();
+        for (int c = threadIdx.x; c < n; c += blockDim.x) {
+            if (sh.ckey[c] > thr_key) sh.sortbuf[atomicAdd(&gcount, 1)] = sh.ckey[c];
+        }
+        __syncthreads();
+        const int g = gcount;
+        block_sort_desc(sh, g);
+        for (int i = g + threadIdx.x; i < rank; i += blockDim.x) sh.sortbuf[i] = thr_key;
+        __syncthreads();
+        rs.theta = top_p_threshold(sh, rank, K, top_p, thr);
+    }
+    const uint32_t theta_key = nvs::float_key(rs.theta);
+    rs.dense = !(fits || rs.theta > thr);
+    float z = 0.f;
+    if (!rs.dense) {
+        for (int c = threadIdx.x; c < n; c += blockDim.x)
+            if (sh.ckey[c] >= theta_key) z += expf(nvs::key_float(sh.ckey[c]) - rs.m);
+    } else {
+        for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
+            float v[kVpt];
+            load_vals<DT>(row, e0, a.vocab, vec, v);
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) {
+                const float s = scale_logit(v[vi], temp, unit_temp);
+                if (sel_key(s) >= theta_key && sel_key(s) != 0u) z += expf(s - rs.m);
+            }
+        }
+    }
+    rs.z = block_sum(z, sh);
+    return rs;
+}
+
+template <int DT, int MODE>
+__global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
+    __shared__ SelShared sh;
+    const int64_t t = blockIdx.x;
+    if (threadIdx.x == 0) {
+        sh.count = 0;
+        sh.overflow = 0;
+        sh.loc[0] = sh.loc[1] = sh.loc[3] = 0;
+        sh.loc[2] = 1;
+    }
+    __syncthreads();
+    int64_t prow;
+    if constexpr (MODE == kModeAccept) {
+        locate(a, t, sh);
+        prow = sh.loc[0];
+    } else {
+        prow = t / a.pos_per_param;
+    }
+    const float temp = a.temps != nullptr ? a.temps[prow] : 1.f;
+    const bool unit_temp = (temp == 1.f);
+    const int64_t tk = a.top_k != nullptr ? a.top_k[prow] : 0;
+    const float top_p = a.top_p != nullptr ? a.top_p[prow] : 1.f;
+    const int K = static_cast<int>(min(static_cast<int64_t>(a.max_top_k), a.vocab));
+    const bool truncating = K > 0 && tk > 0;
+    const int rank = truncating ? static_cast<int>(min(tk, static_cast<int64_t>(K))) : 0;
+    const char* row = static_cast<const char*>(a.logits) + t * a.row_stride * nvs::dtype_size(DT);
+    const bool vec = nvs::aligned16(a.logits) && ((a.row_stride * nvs::dtype_size(DT)) % 16 == 0);
+
+    RowStats rs;
+    rs.dense = !truncating;
+    rs.theta = -INFINITY;
+    if (!truncating) {
+        // online max / sum-exp over the whole row
+        float m = -INFINITY, z = 0.f;
+        for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
+            float v[kVpt];
+            load_vals<DT>(row, e0, a.vocab, vec, v);
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) {
+                const float s = scale_logit(v[vi], temp, unit_temp);
+                if (s != s) continue;
+                if (s > m) {
+                    z = z * expf(m - s) + 1.f;
+                    m = s;
+                } else {
+                    z += expf(s - m);
+                }
+            }
+        }
+        const uint32_t mk = block_max_u32(m == -INFINITY ? 0u : nvs::float_key(m), sh);
+        const float mall = mk == 0u ? -INFINITY : nvs::key_float(mk);
+        const float mu = (mall == -INFINITY) ? 0.f : mall;
+        const float zz = (m == -INFINITY) ? 0.f : z * expf(m - mu);
+        rs.z = block_sum(zz, sh);
+        rs.m = mall;
+    } else {
+        // ---- one pass: candidate list of everything >= a lower bound of the K-th largest
+        uint32_t tau_key = 0u;
+        float vcur[kVpt];
+        load_vals<DT>(row, 0, a.vocab, vec, vcur);
+        for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
+            float vnext[kVpt];
+            const bool more = e0 + kBatch < a.vocab;
+            if (more) load_vals<DT>(row, e0 + kBatch, a.vocab, vec, vnext);
+            uint32_t keys[kVpt];
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) keys[vi] = sel_key(scale_logit(vcur[vi], temp, unit_temp));
+            if (e0 == 0) {
+                // initial bound: each wave's ceil(K/8)-th largest lane maximum, smallest over the waves
+                uint32_t tmax = 0u;
+#pragma unroll
+                for (int vi = 0; vi < kVpt; ++vi) tmax = max(tmax, keys[vi]);
+                const int rw = (K + kSelWaves - 1) / kSelWaves;
+                uint32_t bound = 0u;
+                if (rw <= 64) {
+                    const uint32_t sorted = wave_sort_desc(tmax);
+                    bound = static_cast<uint32_t>(__shfl(static_cast<int>(sorted), rw - 1));
+                }
+                if (lane_id() == 0) sh.ured[threadIdx.x >> 6] = bound;
+                __syncthreads();
+                uint32_t b = 0xffffffffu;
+                for (int w = 0; w < kSelWaves; ++w) b = min(b, sh.ured[w]);
+                tau_key = b;
+                __syncthreads();
+            }
+            append_candidates<DT>(sh, keys, e0, tau_key);
+            __syncthreads();
+            const int cnt = sh.count;
+            const int ovf = sh.overflow;
+            __syncthreads();  // everyone has read the count before the next batch appends
+            if (ovf) break;
+            if (cnt > kCap / 2) {
+                // prune to the exact K-th largest of the list
+                const int n = sh.count;
+                auto each = [&](auto&& fn) {
+                    for (int c = threadIdx.x; c < n; c += blockDim.x) fn(sh.ckey[c]);
+                };
+                uint32_t ng, ne;
+                const uint32_t kth = radix_select(each, static_cast<uint32_t>(K), sh, &ng, &ne);
+                tau_key = max(tau_key, kth);
+                compact_candidates(sh, tau_key);
+                const int kept = sh.count;
+                __syncthreads();
+                if (kept > kCap / 2) {
+                    // more than half the list is tied at the bound: let the exact path handle the row
+                    if (threadIdx.x == 0) sh.overflow = 1;
+                    __syncthreads();
+                    break;
+                }
+            }
+            if (more) {
+#pragma unroll
+                for (int vi = 0; vi < kVpt; ++vi) vcur[vi] = vnext[vi];
+            }
+        }
+        __syncthreads();
+        if (sh.overflow) {
+            rs = exact_row_stats<DT>(a, row, vec, temp, unit_temp, rank, K, top_p, sh);
+        } else {
+            const int n = sh.count;
+            auto each = [&](auto&& fn) {
+                for (int c = threadIdx.x; c < n; c += blockDim.x) fn(sh.ckey[c]);
+            };
+            uint32_t ng, ne;
+            const uint32_t thr_key = radix_select(each, static_cast<uint32_t>(rank), sh, &ng, &ne);
+            uint32_t mk = 0u;
+            for (int c = threadIdx.x; c < n; c += blockDim.x) mk = max(mk, sh.ckey[c]);
+            mk = block_max_u32(mk, sh);
+            rs.m = nvs::key_float(mk);
+            const float thr = nvs::key_float(thr_key);
+            rs.theta = thr;
+            if (a.has_top_p) {
+                __shared__ int gcount;
+                if (threadIdx.x == 0) gcount = 0;
+                __syncthreads();
+                for (int c = threadIdx.x; c < n; c += blockDim.x)
+                    if (sh.ckey[c] > thr_key) sh.sortbuf[atomicAdd(&gcount, 1)] = sh.ckey[c];
+                __syncthreads();
+                const int g = gcount;
+                block_sort_desc(sh, g);
+                for (int i = g + threadIdx.x; i < rank; i += blockDim.x) sh.sortbuf[i] = thr_key;
+                __syncthreads();
+                rs.theta = top_p_threshold(sh, rank, K, top_p, thr);
+            }
+            const uint32_t theta_key = nvs::float_key(rs.theta);
+            float z = 0.f;
+            for (int c = threadIdx.x; c < n; c += blockDim.x)
+                if (sh.ckey[c] >= theta_key) z += expf(nvs::key_float(sh.ckey[c]) - rs.m);
+            rs.z = block_sum(z, sh);
+            rs.dense = false;
+        }
+    }
+
+    const uint32_t theta_key = rs.theta == -INFINITY ? 0u : nvs::float_key(rs.theta);
+    const float mu = (rs.m == -INFINITY) ? 0.f : rs.m;
+
+    if constexpr (MODE == kModeProbs || MODE == kModeTruncate) {
+        float* orow = a.out + t * a.out_stride;
+        for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
+            float v[kVpt];
+            load_vals<DT>(row, e0, a.vocab, vec, v);
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) {
+                const int64_t e = val_index<DT>(e0, vi);
+                if (e >= a.vocab) continue;
+                const float s = scale_logit(v[vi], temp, unit_temp);
+                const bool kept = sel_key(s) >= theta_key;
+                if constexpr (MODE == kModeProbs) {
+                    orow[e] = kept ? expf(s - mu) / rs.z : 0.f;
+                } else {
+                    orow[e] = kept ? s : -INFINITY;
+                }
+            }
+        }
+        return;
+    } else {
+        // ---- fused accept: this position's accept test and race
+        const int64_t b = sh.loc[0], j = sh.loc[1], L = sh.loc[2];
+        const int kd = a.k;
+        const bool bonus = (j >= L - 1) || (j >= kd);
+        int acc = 0;
+        if (threadIdx.x == 0 && j < L - 1 && j < kd) {
+            const int64_t d = a.drafts[b * kd + j];
+            if (d >= 0 && d < a.vocab) {  // an out-of-vocabulary draft is never accepted
+                const float sd = scale_logit(nvs::load_as_float<DT>(row, d), temp, unit_temp);
+                const float pd = (sel_key(sd) >= theta_key && sel_key(sd) != 0u) ? expf(sd - mu) / rs.z : 0.f;
+                const float qd = a.q[(b * kd + j) * a.vocab + d];
+                acc = (a.uniforms[b * kd + j] * qd < pd) ? 1 : 0;
+            }
+        }
+        uint64_t best = 0;
+        if (!rs.dense) {
+            const int n = min(sh.count, kCap);
+            const float* qrow = a.q + (b * kd + (bonus ? 0 : j)) * a.vocab;
+            const float* erow = a.noise + b * a.vocab;
+            for (int c = threadIdx.x; c < n; c += blockDim.x) {
+                const uint32_t key = sh.ckey[c];
+                if (key < theta_key) continue;
+                const int64_t i = sh.cidx[c];
+                const float p = expf(nvs::key_float(key) - mu) / rs.z;
+                const float w = bonus ? p : fmaxf(p - qrow[i], 0.f);
+                const float score = w / erow[i];
+                const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+                                     static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
+                best = best > k64 ? best : k64;
+            }
+        }
+        best = block_max_u64(best, sh);
+        if (threadIdx.x == 0) {
+            PosRecord r;
+            r.m = rs.m;
+            r.z = rs.z;
+            r.theta = rs.theta;
+            r.temp = temp;
+            r.flags = rs.dense ? kFlagDense : 0;
+            r.acc = acc;
+            int64_t winner = 0;
+            if (!rs.dense && best != 0) {
+                const float score = nvs::key_float(static_cast<uint32_t>(best >> 32));
+                // all weights zero: torch's argmax over the zero vector is index 0
+                winner = (score > 0.f) ? static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best))
+                                       : int64_t{0};
+            }
+            r.race = winner;
+            a.rec[t] = r;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- fused accept: finalize per batch row
+
+struct FinArgs {
+    const void* logits;
+    int64_t row_stride;
+    int64_t vocab;
+    const float* q;
+    const int64_t* drafts;
+    const int64_t* lens;
+    const float* noise;
+    int64_t batch;
+    int64_t n_pos;
+    int k;
+    const PosRecord* rec;
+    int64_t* n_accept;
+    int64_t* tail;
+};
+
+__device__ __forceinline__ int64_t row_start(const int64_t* lens, int64_t b, int k) {
+    // exclusive prefix of lens over rows < b (workgroup reduction)
+    __shared__ int64_t part[4];
+    if (lens == nullptr) return b * (k + 1);
+    int64_t s = 0;
+    for (int64_t i = threadIdx.x; i < b; i += blockDim.x) s += lens[i];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    int64_t tot = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += part[w];
+    return tot;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void accept_finalize_kernel(FinArgs a) {
+    __shared__ uint64_t red[4];
+    const int64_t b = blockIdx.x;
+    const int kd = a.k;
+    const int64_t start = row_start(a.lens, b, kd);
+    const int64_t L = a.lens != nullptr ? a.lens[b] : kd + 1;
+    int64_t n = 0;
+    while (n < L - 1 && n < kd && start + n < a.n_pos && a.rec[start + n].acc) ++n;
+    const int64_t pos = min(start + n, a.n_pos - 1);
+    const PosRecord r = a.rec[pos];
+    int64_t winner = r.race;
+    if (r.flags & kFlagDense) {
+        const bool bonus = (n == L - 1);
+        const int64_t qn = n < kd - 1 ? n : kd - 1;
+        const float* qrow = a.q + (b * kd + qn) * a.vocab;
+        const float* erow = a.noise + b * a.vocab;
+        const char* row = static_cast<const char*>(a.logits) + pos * a.row_stride * nvs::dtype_size(DT);
+        const uint32_t theta_key = r.theta == -INFINITY ? 0u : nvs::float_key(r.theta);
+        const float mu = (r.m == -INFINITY) ? 0.f : r.m;
+        const bool unit_temp = (r.temp == 1.f);
+        uint64_t best = 0;
+        for (int64_t i = threadIdx.x; i < a.vocab; i += blockDim.x) {
+            const float s = scale_logit(nvs::load_as_float<DT>(row, i), r.temp, unit_temp);
+            const float p = (sel_key(s) >= theta_key && s == s) ? expf(s - mu) / r.z : 0.f;
+            const float w = bonus ? p : fmaxf(p - qrow[i], 0.f);
+            const float score = w / erow[i];
+            const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+                                 static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
+            best = best > k64 ? best : k64;
+        }
+        best = wave_max_u64(best);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+        __syncthreads();
+        uint64_t all = 0;
+        for (int w = 0; w < 4; ++w) all = red[w] > all ? red[w] : all;
+        winner = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(all));
+    }
+    if (threadIdx.x == 0) {
+        a.n_accept[b] = n;
+        a.tail[b] = winner;
+    }
+}
+
+// ---------------------------------------------------------------- dense race kernels
+
+struct RaceArgs {
+    // w(i) = bonus ? p[prow, i] : max(p[prow, i] - q[qrow, i], 0)   (accept)   or   w[r, i]   (race)
+    const float* p;
+    int64_t p_stride;
+    const float* q;
+    const float* noise;
+    int64_t noise_stride;
+    const int64_t* drafts;
+    const int64_t* lens;
+    const float* uniforms;
+    int64_t rows;
+    int64_t n_pos;
+    int k;
+    int64_t vocab;
+    int n_chunks;
+    uint64_t* partial;  // [rows, n_chunks]
+    int64_t* n_accept;
+    int64_t* out;
+};
+
+// Accepted prefix of row b over dense p (accept_random_varlen's gathers, spec_sampler.py:134-143).
+__device__ int64_t accepted_prefix(const RaceArgs& a, int64_t b, int64_t start, int64_t L) {
+    __shared__ int64_t n_sh;
+    if (threadIdx.x == 0) {
+        int64_t n = 0;
+        while (n < L - 1 && n < a.k && start + n < a.n_pos) {
+            const int64_t d = a.drafts[b * a.k + n];
+            if (d < 0 || d >= a.vocab) break;  // an out-of-vocabulary draft is never accepted
+            const float pd = a.p[(start + n) * a.p_stride + d];
+            const float qd = a.q[(b * a.k + n) * a.vocab + d];
+            if (!(a.uniforms[b * a.k + n] * qd < pd)) break;
+            ++n;
+        }
+        n_sh = n;
+    }
+    __syncthreads();
+    return n_sh;
+}
+
+template <bool kAccept>
+__global__ __launch_bounds__(256) void race_chunk_kernel(RaceArgs a) {
+    __shared__ uint64_t red[4];
+    const int64_t r = blockIdx.y;
+    const int c = blockIdx.x;
+    const float* wrow;
+    const float* qrow = nullptr;
+    bool bonus = true;
+    if constexpr (kAccept) {
+        const int64_t start = row_start(a.lens, r, a.k);
+        const int64_t L = a.lens != nullptr ? a.lens[r] : a.k + 1;
+        const int64_t n = accepted_prefix(a, r, start, L);
+        bonus = (n == L - 1);
+        wrow = a.p + min(start + n, a.n_pos - 1) * a.p_stride;
+        qrow = a.q + (r * a.k + (n < a.k - 1 ? n : a.k - 1)) * a.vocab;
+    } else {
+        wrow = a.p + r * a.p_stride;
+    }
+    const float* erow = a.noise + r * a.noise_stride;
+    const int64_t i0 = static_cast<int64_t>(c) * kRaceChunk;
+    const int64_t i1 = min(i0 + kRaceChunk, a.vocab);
+    uint64_t best = 0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+        float w = wrow[i];
+        if (kAccept && !bonus) w = fmaxf(w - qrow[i], 0.f);
+        const float score = w / erow[i];
+        const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+                             static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
+        best = best > k64 ? best : k64;
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t all = 0;
+        for (int w = 0; w < 4; ++w) all = red[w] > all ? red[w] : all;
+        a.partial[r * a.n_chunks + c] = all;
+    }
+}
+
+template <bool kAccept>
+__global__ __launch_bounds__(64) void race_merge_kernel(RaceArgs a) {
+    const int64_t r = blockIdx.x;
+    uint64_t best = 0;
+    for (int c = threadIdx.x; c < a.n_chunks; c += 64) {
+        const uint64_t v = a.partial[r * a.n_chunks + c];
+        best = best > v ? best : v;
+    }
+    best = wave_max_u64(best);
+    int64_t n = 0;
+    if constexpr (kAccept) {
+        // recompute the prefix (k gathers) rather than carrying it between kernels
+        __shared__ int64_t start_sh;
+        if (threadIdx.x == 0) {
+            int64_t s = 0;
+            if (a.lens != nullptr) {
+                for (int64_t i = 0; i < r; ++i) s += a.lens[i];
+            } else {
+                s = r * (a.k + 1);
+            }
+            start_sh = s;
+        }
+        __syncthreads();
+        const int64_t L = a.lens != nullptr ? a.lens[r] : a.k + 1;
+        n = accepted_prefix(a, r, start_sh, L);
+    }
+    if (threadIdx.x == 0) {
+        a.out[r] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
+        if constexpr (kAccept) a.n_accept[r] = n;
+    }
+}
+
+// ---------------------------------------------------------------- greedy
+
+template <int DT>
+__global__ __launch_bounds__(kSelThreads) void argmax_kernel(const void* logits, int64_t row_stride, int64_t vocab,
+                                                             int64_t* tokens) {
+    __shared__ uint64_t red[kSelWaves];
+    const int64_t t = blockIdx.x;
+    const char* row = static_cast<const char*>(logits) + t * row_stride * nvs::dtype_size(DT);
+    const bool vec = nvs::aligned16(logits) && ((row_stride * nvs::dtype_size(DT)) % 16 == 0);
+    uint64_t best = 0;
+    for (int64_t e0 = 0; e0 < vocab; e0 += kBatch) {
+        float v[kVpt];
+        load_vals<DT>(row, e0, vocab, vec, v);
+#pragma unroll
+        for (int vi = 0; vi < kVpt; ++vi) {
+            const int64_t e = val_index<DT>(e0, vi);
+            if (e >= vocab) continue;
+            // torch's argmax: NaN counts as the maximum; first index on ties
+            const uint32_t key = (v[vi] != v[vi]) ? 0xffffffffu : nvs::float_key(v[vi]);
+            const uint64_t k64 = (static_cast<uint64_t>(key) << 32) |
+                                 static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(e));
+            best = best > k64 ? best : k64;
+        }
+    }
+    best = wave_max_u64(best);
+    if (lane_id() == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t all = 0;
+        for (int w = 0; w < kSelWaves; ++w) all = red[w] > all ? red[w] : all;
+        tokens[t] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(all));
+    }
+}
+
+__global__ __launch_bounds__(64) void greedy_finalize_kernel(const int64_t* tokens, const int64_t* drafts,
+                                                             const int64_t* lens, int64_t batch, int64_t n_pos,
+                                                             int k, int64_t* n_accept, int64_t* tail) {
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (b >= batch) return;
+    int64_t start = 0;
+    if (lens != nullptr) {
+        for (int64_t i = 0; i < b; ++i) start += lens[i];
+    } else {
+        start = b * (k + 1);
+    }
+    const int64_t L = lens != nullptr ? lens[b] : k + 1;
+    int64_t n = 0;
+    while (n < L - 1 && n < k && start + n < n_pos && tokens[start + n] == drafts[b * k + n]) ++n;
+    n_accept[b] = n;
+    tail[b] = tokens[min(start + n, n_pos - 1)];
+}
+
+// ---------------------------------------------------------------- host side
+
+int check_dtype(int dt) {
+    NVS_CHECK(dt == NVS_DTYPE_F32 || dt == NVS_DTYPE_BF16 || dt == NVS_DTYPE_F16, NVS_ERR_INVALID,
+              "sampler: unknown logits dtype %d", dt);
+    return NVS_OK;
+}
+
+int check_topk(int max_top_k) {
+    NVS_CHECK(max_top_k >= 0, NVS_ERR_INVALID, "sampler: max_top_k %d is negative", max_top_k);
+    NVS_CHECK(max_top_k <= kMaxTopK, NVS_ERR_UNSUPPORTED, "sampler: max_top_k %d above %d", max_top_k, kMaxTopK);
+    return NVS_OK;
+}
+
+template <int MODE>
+int launch_select(int dt, const SelArgs& a, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(a.n_pos));
+    switch (dt) {
+        case NVS_DTYPE_F32: hipLaunchKernelGGL((select_kernel<NVS_DTYPE_F32, MODE>), grid, dim3(kSelThreads), 0, s, a); break;
+        case NVS_DTYPE_BF16: hipLaunchKernelGGL((select_kernel<NVS_DTYPE_BF16, MODE>), grid, dim3(kSelThreads), 0, s, a); break;
+        default: hipLaunchKernelGGL((select_kernel<NVS_DTYPE_F16, MODE>), grid, dim3(kSelThreads), 0, s, a); break;
+    }
+    return nvs::check_launch("sampler select kernel");
+}
+
+int64_t race_chunks(int64_t vocab) { return (vocab + kRaceChunk - 1) / kRaceChunk; }
+
+}  // namespace
+
+// ================================================================ entry points
+
+extern "C" int nvs_probs_from_logits_workspace_size(int64_t n_pos, int64_t vocab, int max_top_k, size_t* bytes) {
+    nvs::clear_error();
+    NVS_CHECK(bytes != nullptr, NVS_ERR_INVALID, "probs_from_logits_workspace_size: bytes is NULL");
+    NVS_CHECK(n_pos >= 0 && vocab >= 0, NVS_ERR_INVALID, "probs_from_logits: negative size");
+    const int st = check_topk(max_top_k);
+    if (st != NVS_OK) return st;
+    *bytes = 0;
+    return NVS_OK;
+}
+
+static int common_select_checks(const void* logits, int64_t row_stride, int64_t n_pos, int64_t vocab,
+                                int64_t pos_per_param, int max_top_k, const int64_t* top_k) {
+    NVS_CHECK(n_pos >= 0 && vocab > 0, NVS_ERR_INVALID, "sampler: bad sizes n_pos=%lld vocab=%lld",
+              (long long)n_pos, (long long)vocab);
+    NVS_CHECK(vocab < 0x7fffffffLL, NVS_ERR_UNSUPPORTED, "sampler: vocab %lld too large", (long long)vocab);
+    NVS_CHECK(row_stride >= vocab, NVS_ERR_INVALID, "sampler: row stride %lld < vocab %lld", (long long)row_stride,
+              (long long)vocab);
+    NVS_CHECK(pos_per_param >= 1, NVS_ERR_INVALID, "sampler: pos_per_param must be >= 1");
+    NVS_CHECK(n_pos <= 0x7fffffffLL, NVS_ERR_UNSUPPORTED, "sampler: too many positions");
+    NVS_CHECK(n_pos == 0 || logits != nullptr, NVS_ERR_INVALID, "sampler: logits is NULL");
+    NVS_CHECK(max_top_k == 0 || top_k != nullptr, NVS_ERR_INVALID, "sampler: max_top_k > 0 needs top_k");
+    return check_topk(max_top_k);
+}
+
+extern "C" int nvs_probs_from_logits(const void* logits, int logits_dtype, int64_t logits_row_stride, int64_t n_pos,
+                                     int64_t vocab, int64_t pos_per_param, const float* temperatures,
+                                     const int64_t* top_k, const float* top_p, int max_top_k, int has_top_p,
+                                     float* probs, void* workspace, size_t workspace_bytes, void* stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    nvs::clear_error();
+    int st = check_dtype(logits_dtype);
+    if (st != NVS_OK) return st;
+    st = common_select_checks(logits, logits_row_stride, n_pos, vocab, pos_per_param, max_top_k, top_k);
+    if (st != NVS_OK) return st;
+    NVS_CHECK(temperatures != nullptr, NVS_ERR_INVALID, "probs_from_logits: temperatures is NULL (greedy batch)");
+    NVS_CHECK(!has_top_p || top_p != nullptr, NVS_ERR_INVALID, "probs_from_logits: has_top_p needs top_p");
+    NVS_CHECK(n_pos == 0 || probs != nullptr, NVS_ERR_INVALID, "probs_from_logits: probs is NULL");
+    if (n_pos == 0) return NVS_OK;
+    SelArgs a{};
+    a.logits = logits;
+    a.row_stride = logits_row_stride;
+    a.n_pos = n_pos;
+    a.vocab = vocab;
+    a.temps = temperatures;
+    a.top_k = max_top_k > 0 ? top_k : nullptr;
+    a.top_p = top_p;
+    a.max_top_k = max_top_k;
+    a.has_top_p = has_top_p && max_top_k > 0;
+    a.pos_per_param = pos_per_param;
+    a.out = probs;
+    a.out_stride = vocab;
+    return launch_select<kModeProbs>(logits_dtype, a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nvs_truncate_logits(const float* scaled, int64_t scaled_row_stride, int64_t n_pos, int64_t vocab,
+                                   int64_t pos_per_param, const int64_t* top_k, const float* top_p, int max_top_k,
+                                   int has_top_p, float* out, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    nvs::clear_error();
+    int st = common_select_checks(scaled, scaled_row_stride, n_pos, vocab, pos_per_param, max_top_k, top_k);
+    if (st != NVS_OK) return st;
+    NVS_CHECK(!has_top_p || top_p != nullptr, NVS_ERR_INVALID, "truncate_logits: has_top_p needs top_p");
+    NVS_CHECK(n_pos == 0 || out != nullptr, NVS_ERR_INVALID, "truncate_logits: out is NULL");
+    if (n_pos == 0) return NVS_OK;
+    SelArgs a{};
+    a.logits = scaled;
+    a.row_stride = scaled_row_stride;
+    a.n_pos = n_pos;
+    a.vocab = vocab;
+    a.temps = nullptr;
+    a.top_k = max_top_k > 0 ? top_k : nullptr;
+    a.top_p = top_p;
+    a.max_top_k = max_top_k;
+    a.has_top_p = has_top_p && max_top_k > 0;
+    a.pos_per_param = pos_per_param;
+    a.out = out;
+    a.out_stride = vocab;
+    return launch_select<kModeTruncate>(NVS_DTYPE_F32, a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nvs_race_workspace_size(int64_t n_rows, int64_t vocab, size_t* bytes) {
+    nvs::clear_error();
+    NVS_CHECK(bytes != nullptr && n_rows >= 0 && vocab >= 0, NVS_ERR_INVALID, "race_workspace_size: bad args");
+    *bytes = static_cast<size_t>(n_rows) * race_chunks(vocab) * sizeof(uint64_t);
+    return NVS_OK;
+}
+
+extern "C" int nvs_race(const float* weights, int64_t weights_row_stride, const float* noise,
+                        int64_t noise_row_stride, int64_t n_rows, int64_t vocab, int64_t* out, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+    nvs::clear_error();
+    NVS_CHECK(n_rows >= 0 && vocab > 0 && vocab < 0x7fffffffLL, NVS_ERR_INVALID, "race: bad sizes");
+    NVS_CHECK(n_rows <= 65535, NVS_ERR_UNSUPPORTED, "race: more than 65535 rows");
+    if (n_rows == 0) return NVS_OK;
+    NVS_CHECK(weights && noise && out, NVS_ERR_INVALID, "race: null pointer");
+    NVS_CHECK(weights_row_stride >= vocab && noise_row_stride >= vocab, NVS_ERR_INVALID, "race: bad row strides");
+    size_t need = 0;
+    nvs_race_workspace_size(n_rows, vocab, &need);
+    NVS_CHECK(workspace != nullptr && workspace_bytes >= need, NVS_ERR_WORKSPACE,
+              "race: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    RaceArgs a{};
+    a.p = weights;
+    a.p_stride = weights_row_stride;
+    a.noise = noise;
+    a.noise_stride = noise_row_stride;
+    a.rows = n_rows;
+    a.vocab = vocab;
+    a.n_chunks = static_cast<int>(race_chunks(vocab));
+    a.partial = static_cast<uint64_t*>(workspace);
+    a.out = out;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(race_chunk_kernel<false>, dim3(a.n_chunks, n_rows), dim3(256), 0, s, a);
+    int st = nvs::check_launch("race chunk kernel");
+    if (st != NVS_OK) return st;
+    hipLaunchKernelGGL(race_merge_kernel<false>, dim3(n_rows), dim3(64), 0, s, a);
+    return nvs::check_launch("race merge kernel");
+}
+
+extern "C" int nvs_accept_random_workspace_size(int64_t batch, int64_t vocab, size_t* bytes) {
+    return nvs_race_workspace_size(batch, vocab, bytes);
+}
+
+static int accept_common_checks(const int64_t* drafts, int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
+                                int64_t* n_accept, int64_t* tail) {
+    NVS_CHECK(batch >= 0 && num_drafts >= 1 && n_pos >= 0 && vocab > 0, NVS_ERR_INVALID,
+              "accept: bad sizes batch=%lld k=%d n_pos=%lld vocab=%lld", (long long)batch, num_drafts,
+              (long long)n_pos, (long long)vocab);
+    NVS_CHECK(vocab < 0x7fffffffLL && batch <= 65535, NVS_ERR_UNSUPPORTED, "accept: sizes too large");
+    NVS_CHECK(batch == 0 || (drafts && n_accept && tail), NVS_ERR_INVALID, "accept: null pointer");
+    return NVS_OK;
+}
+
+extern "C" int nvs_accept_random(const float* p, const float* q, const int64_t* drafts, const int64_t* verified_lens,
+                                 const float* uniforms, const float* noise, int64_t batch, int num_drafts,
+                                 int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    nvs::clear_error();
+    int st = accept_common_checks(drafts, batch, num_drafts, n_pos, vocab, n_accept, tail);
+    if (st != NVS_OK) return st;
+    if (batch == 0) return NVS_OK;
+    NVS_CHECK(p && q && uniforms && noise, NVS_ERR_INVALID, "accept_random: null pointer");
+    NVS_CHECK(verified_lens != nullptr || n_pos == batch * (num_drafts + 1), NVS_ERR_INVALID,
+              "accept_random: p has %lld positions, expected batch*(k+1) = %lld", (long long)n_pos,
+              (long long)(batch * (num_drafts + 1)));
+    size_t need = 0;
+    nvs_race_workspace_size(batch, vocab, &need);
+    NVS_CHECK(workspace != nullptr && workspace_bytes >= need, NVS_ERR_WORKSPACE,
+              "accept_random: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    RaceArgs a{};
+    a.p = p;
+    a.p_stride = vocab;
+    a.q = q;
+    a.noise = noise;
+    a.noise_stride = vocab;
+    a.drafts = drafts;
+    a.lens = verified_lens;
+    a.uniforms = uniforms;
+    a.rows = batch;
+    a.n_pos = n_pos;
+    a.k = num_drafts;
+    a.vocab = vocab;
+    a.n_chunks = static_cast<int>(race_chunks(vocab));
+    a.partial = static_cast<uint64_t*>(workspace);
+    a.n_accept = n_accept;
+    a.out = tail;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(race_chunk_kernel<true>, dim3(a.n_chunks, batch), dim3(256), 0, s, a);
+    st = nvs::check_launch("accept_random chunk kernel");
+    if (st != NVS_OK) return st;
+    hipLaunchKernelGGL(race_merge_kernel<true>, dim3(batch), dim3(64), 0, s, a);
+    return nvs::check_launch("accept_random merge kernel");
+}
+
+extern "C" int nvs_accept_greedy_workspace_size(int64_t n_pos, int64_t vocab, size_t* bytes) {
+    nvs::clear_error();
+    (void)vocab;
+    NVS_CHECK(bytes != nullptr && n_pos >= 0, NVS_ERR_INVALID, "accept_greedy_workspace_size: bad args");
+    *bytes = static_cast<size_t>(n_pos) * sizeof(int64_t);
+    return NVS_OK;
+}
+
+extern "C" int nvs_accept_greedy(const void* logits, int logits_dtype, int64_t logits_row_stride,
+                                 const int64_t* drafts, const int64_t* verified_lens, int64_t batch, int num_drafts,
+                                 int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    nvs::clear_error();
+    int st = check_dtype(logits_dtype);
+    if (st != NVS_OK) return st;
+    st = accept_common_checks(drafts, batch, num_drafts, n_pos, vocab, n_accept, tail);
+    if (st != NVS_OK) return st;
+    if (batch == 0) return NVS_OK;
+    NVS_CHECK(logits != nullptr && logits_row_stride >= vocab, NVS_ERR_INVALID, "accept_greedy: bad logits");
+    NVS_CHECK(verified_lens != nullptr || n_pos == batch * (num_drafts + 1), NVS_ERR_INVALID,
+              "accept_greedy: logits have %lld positions, expected batch*(k+1) = %lld", (long long)n_pos,
+              (long long)(batch * (num_drafts + 1)));
+    NVS_CHECK(n_pos <= 0x7fffffffLL, NVS_ERR_UNSUPPORTED, "accept_greedy: too many positions");
+    size_t need = static_cast<size_t>(n_pos) * sizeof(int64_t);
+    NVS_CHECK(workspace != nullptr && workspace_bytes >= need, NVS_ERR_WORKSPACE,
+              "accept_greedy: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    int64_t* tokens = static_cast<int64_t*>(workspace);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid(static_cast<unsigned>(n_pos));
+    switch (logits_dtype) {
+        case NVS_DTYPE_F32: hipLaunchKernelGGL(argmax_kernel<NVS_DTYPE_F32>, grid, dim3(kSelThreads), 0, s, logits, logits_row_stride, vocab, tokens); break;
+        case NVS_DTYPE_BF16: hipLaunchKernelGGL(argmax_kernel<NVS_DTYPE_BF16>, grid, dim3(kSelThreads), 0, s, logits, logits_row_stride, vocab, tokens); break;
+        default: hipLaunchKernelGGL(argmax_kernel<NVS_DTYPE_F16>, grid, dim3(kSelThreads), 0, s, logits, logits_row_stride, vocab, tokens); break;
+    }
+    st = nvs::check_launch("accept_greedy argmax kernel");
+    if (st != NVS_OK) return st;
+    hipLaunchKernelGGL(greedy_finalize_kernel, dim3(static_cast<unsigned>((batch + 63) / 64)), dim3(64), 0, s, tokens,
+                       drafts, verified_lens, batch, n_pos, num_drafts, n_accept, tail);
+    return nvs::check_launch("accept_greedy finalize kernel");
+}
+
+extern "C" int nvs_spec_accept_workspace_size(int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
+                                              int max_top_k, size_t* bytes) {
+    nvs::clear_error();
+    (void)batch;
+    (void)num_drafts;
+    (void)vocab;
+    NVS_CHECK(bytes != nullptr && n_pos >= 0, NVS_ERR_INVALID, "spec_accept_workspace_size: bad args");
+    const int st = check_topk(max_top_k);
+    if (st != NVS_OK) return st;
+    *bytes = static_cast<size_t>(n_pos) * sizeof(PosRecord);
+    return NVS_OK;
+}
+
+extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_stride,
+                               const float* temperatures, const int64_t* top_k, const float* top_p, int max_top_k,
+                               int has_top_p, const float* q, const int64_t* drafts, const int64_t* verified_lens,
+                               const float* uniforms, const float* noise, int64_t batch, int num_drafts,
+                               int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    nvs::clear_error();
+    int st = check_dtype(logits_dtype);
+    if (st != NVS_OK) return st;
+    st = accept_common_checks(drafts, batch, num_drafts, n_pos, vocab, n_accept, tail);
+    if (st != NVS_OK) return st;
+    st = common_select_checks(logits, logits_row_stride, n_pos, vocab, 1, max_top_k, top_k);
+    if (st != NVS_OK) return st;
+    if (batch == 0) return NVS_OK;
+    NVS_CHECK(temperatures && q && uniforms && noise, NVS_ERR_INVALID, "spec_accept: null pointer");
+    NVS_CHECK(!has_top_p || top_p != nullptr, NVS_ERR_INVALID, "spec_accept: has_top_p needs top_p");
+    NVS_CHECK(verified_lens != nullptr || n_pos == batch * (num_drafts + 1), NVS_ERR_INVALID,
+              "spec_accept: logits have %lld positions, expected batch*(k+1) = %lld", (long long)n_pos,
+              (long long)(batch * (num_drafts + 1)));
+    const size_t need = static_cast<size_t>(n_pos) * sizeof(PosRecord);
+    NVS_CHECK(workspace != nullptr && workspace_bytes >= need, NVS_ERR_WORKSPACE,
+              "spec_accept: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    SelArgs a{};
+    a.logits = logits;
+    a.row_stride = logits_row_stride;
+    a.n_pos = n_pos;
+    a.vocab = vocab;
+    a.temps = temperatures;
+    a.top_k = max_top_k > 0 ? top_k : nullptr;
+    a.top_p = top_p;
+    a.max_top_k = max_top_k;
+    a.has_top_p = has_top_p && max_top_k > 0;
+    a.pos_per_param = 1;
+    a.q = q;
+    a.drafts = drafts;
+    a.lens = verified_lens;
+    a.uniforms = uniforms;
+    a.noise = noise;
+    a.batch = batch;
+    a.k = num_drafts;
+    a.rec = static_cast<PosRecord*>(workspace);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    st = launch_select<kModeAccept>(logits_dtype, a, s);
+    if (st != NVS_OK) return st;
+    FinArgs f{};
+    f.logits = logits;
+    f.row_stride = logits_row_stride;
+    f.vocab = vocab;
+    f.q = q;
+    f.drafts = drafts;
+    f.lens = verified_lens;
+    f.noise = noise;
+    f.batch = batch;
+    f.n_pos = n_pos;
+    f.k = num_drafts;
+    f.rec = a.rec;
+    f.n_accept = n_accept;
+    f.tail = tail;
+    switch (logits_dtype) {
+        case NVS_DTYPE_F32: hipLaunchKernelGGL(accept_finalize_kernel<NVS_DTYPE_F32>, dim3(batch), dim3(256), 0, s, f); break;
+        case NVS_DTYPE_BF16: hipLaunchKernelGGL(accept_finalize_kernel<NVS_DTYPE_BF16>, dim3(batch), dim3(256), 0, s, f); break;
+        default: hipLaunchKernelGGL(accept_finalize_kernel<NVS_DTYPE_F16>, dim3(batch), dim3(256), 0, s, f); break;
+    }
+    return nvs::check_launch("spec_accept finalize kernel");
+}

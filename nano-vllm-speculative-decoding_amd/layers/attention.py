@@ -1,0 +1,156 @@
+"""Paged KV store and paged multi-query attention on MI355X, behind the reference's Attention interface.
+
+Mirrors nanovllm/layers/attention.py:
+  store_kvcache(key, value, k_cache, v_cache, slot_mapping)          attention.py:33-40
+  Attention(num_heads, head_dim, scale, num_kv_heads).forward(q,k,v)  attention.py:43-77
+and the two flash-attn entry points that forward calls, with the keyword arguments it passes:
+  paged_attention_varlen(...)        for flash_attn_varlen_func(..., causal=True, block_table=...) (verify branch)
+  paged_attention_with_kvcache(...)  for flash_attn_with_kvcache(q[B, Lq, H, D], ...) (decode / draft-block branch)
+Both run nvs_paged_attention (one HIP launch plus a split combine when a row's keys are split) and
+store_kvcache runs nvs_store_kvcache.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import nn
+
+from .. import _lib
+from ..utils.context import get_context
+
+
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  slot_mapping: torch.Tensor) -> None:
+    """Write token i's K/V rows into cache slot slot_mapping[i] (slot -1 = padding, skipped).
+
+    key/value: [N, Hkv, D] with contiguous rows (value may be a strided view of the fused qkv output);
+    k_cache/v_cache: [blocks, block_size, Hkv, D]; slot_mapping: [N] int32. Same preconditions as the reference
+    (attention.py:36-39)."""
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == D and v_cache.stride(1) == D
+    assert slot_mapping.numel() == N
+    _lib.require_device(key, value, k_cache, v_cache, slot_mapping)
+    assert value.shape == key.shape and k_cache.dtype == key.dtype == value.dtype == v_cache.dtype
+    assert k_cache.is_contiguous() and v_cache.is_contiguous()
+    if slot_mapping.dtype != torch.int32:
+        slot_mapping = slot_mapping.to(torch.int32)
+    if not slot_mapping.is_contiguous():
+        slot_mapping = slot_mapping.contiguous()
+    lib = _lib.load()
+    _lib.check(lib.nvs_store_kvcache(key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
+                                     k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // D,
+                                     slot_mapping.data_ptr(), N, num_heads, head_dim, _lib.dtype_code(key.dtype),
+                                     _lib.stream_of(key)),
+               "store_kvcache")
+
+
+def _paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_table: torch.Tensor,
+                     cu_seqlens_q: torch.Tensor | None, cu_seqlens_k: torch.Tensor | None,
+                     context_lens: torch.Tensor | None, query_len_per_seq: int, num_rows: int, max_seqlen_q: int,
+                     max_seqlen_k: int, softmax_scale: float, causal: bool, out: torch.Tensor | None = None,
+                     workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """q: [T, H, D] (last dim contiguous). Returns out [T, H, D] (written into `out` when given; `workspace`, a
+    uint8 device buffer of at least the planned size, avoids an allocation per call)."""
+    _lib.require_device(q, k_cache, v_cache, block_table, cu_seqlens_q, cu_seqlens_k, context_lens)
+    T, H, D = q.shape
+    assert k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride()
+    _, block_size, Hkv, Dk = k_cache.shape
+    assert Dk == D and H % Hkv == 0
+    assert q.stride(-1) == 1 and k_cache.stride(-1) == 1
+    assert q.dtype == k_cache.dtype == v_cache.dtype
+    for name, t in (("block_table", block_table), ("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_k", cu_seqlens_k),
+                    ("context_lens", context_lens)):
+        if t is not None and t.dtype != torch.int32:
+            raise ValueError(f"{name} must be int32, got {t.dtype}")
+    if block_table.stride(-1) != 1:
+        block_table = block_table.contiguous()
+    for t in (cu_seqlens_q, cu_seqlens_k, context_lens):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("cu_seqlens / context_lens must be contiguous")
+    if out is None:
+        out = torch.empty((T, H, D), dtype=q.dtype, device=q.device)
+    assert out.shape == (T, H, D) and out.dtype == q.dtype and out.stride(-1) == 1
+    lib = _lib.load()
+    nbytes = _lib.size_out()
+    _lib.check(lib.nvs_paged_attention_workspace_size(num_rows, H, Hkv, D, max_seqlen_q, max_seqlen_k,
+                                                      ctypes.byref(nbytes)),
+               "paged_attention_workspace_size")
+    ws = workspace if workspace is not None and workspace.numel() >= nbytes.value else \
+        _lib.workspace(nbytes.value, q.device)
+    _lib.check(lib.nvs_paged_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), T, k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), block_table.data_ptr(), block_table.stride(0),
+        block_table.shape[1], _lib.ptr(cu_seqlens_q), _lib.ptr(cu_seqlens_k), _lib.ptr(context_lens), query_len_per_seq,
+        num_rows, max_seqlen_q, max_seqlen_k, H, Hkv, D, block_size, float(softmax_scale), int(bool(causal)),
+        _lib.dtype_code(q.dtype), out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(ws), nbytes.value,
+        _lib.stream_of(q)),
+        "paged_attention")
+    return out
+
+
+def paged_attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, max_seqlen_q: int,
+                           cu_seqlens_q: torch.Tensor, max_seqlen_k: int, cu_seqlens_k: torch.Tensor,
+                           softmax_scale: float, causal: bool = True,
+                           block_table: torch.Tensor | None = None) -> torch.Tensor:
+    """The call attention.py:67-70 makes with a block table: k, v are the paged caches [blocks, bs, Hkv, D];
+    row r owns queries cu_seqlens_q[r]..cu_seqlens_q[r+1] and cu_seqlens_k[r+1]-cu_seqlens_k[r] keys."""
+    if block_table is None:
+        raise NotImplementedError("nvs_amd implements the paged (block_table) verify branch only; prefill "
+                                  "attention without a prefix cache is outside the verify hot path")
+    return _paged_attention(q, k, v, block_table, cu_seqlens_q, cu_seqlens_k, None, 0, cu_seqlens_q.numel() - 1,
+                            max_seqlen_q, max_seqlen_k, softmax_scale, causal)
+
+
+def paged_attention_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                                 cache_seqlens: torch.Tensor, block_table: torch.Tensor, softmax_scale: float,
+                                 causal: bool = True, max_seqlen_k: int | None = None) -> torch.Tensor:
+    """The call attention.py:72-75 makes: q [B, Lq, H, D] sequence-major, cache_seqlens [B] keys per row.
+    Returns [B, Lq, H, D]. max_seqlen_k bounds every cache_seqlens entry; it defaults to the width of the block
+    table (what the table can address), which keeps the launch independent of device values."""
+    B, Lq, H, D = q.shape
+    if max_seqlen_k is None:
+        max_seqlen_k = block_table.shape[1] * k_cache.shape[1]
+    out = _paged_attention(q.reshape(B * Lq, H, D), k_cache, v_cache, block_table, None, None, cache_seqlens, Lq,
+                           B, Lq, max_seqlen_k, softmax_scale, causal)
+    return out.view(B, Lq, H, D)
+
+
+# The names Attention.forward calls in the reference, for a one-line import swap at that call site.
+flash_attn_varlen_func = paged_attention_varlen
+flash_attn_with_kvcache = paged_attention_with_kvcache
+
+
+class Attention(nn.Module):
+    """attention.py:43-77 on nvs_amd kernels: store the new K/V, then paged attention over the cache."""
+
+    def __init__(self, num_heads, head_dim, scale, num_kv_heads):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.k_cache = self.v_cache = torch.tensor([])
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        context = get_context()
+        k_cache, v_cache = self.k_cache, self.v_cache
+        if k_cache.numel() and v_cache.numel():
+            store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
+        if context.is_prefill:
+            if context.block_tables is None:
+                raise NotImplementedError("nvs_amd Attention serves the paged verify / decode branches; prefill "
+                                          "without a prefix cache is outside the verify hot path")
+            return paged_attention_varlen(q, k_cache, v_cache, max_seqlen_q=context.max_seqlen_q,
+                                          cu_seqlens_q=context.cu_seqlens_q, max_seqlen_k=context.max_seqlen_k,
+                                          cu_seqlens_k=context.cu_seqlens_k, softmax_scale=self.scale, causal=True,
+                                          block_table=context.block_tables)
+        # decode: query_len_per_seq queries per sequence, sequence-major rows
+        o = paged_attention_with_kvcache(q.view(-1, context.query_len_per_seq, self.num_heads, self.head_dim),
+                                         k_cache, v_cache, cache_seqlens=context.context_lens,
+                                         block_table=context.block_tables, softmax_scale=self.scale,
+                                         causal=context.causal)
+        return o.view(-1, self.num_heads, self.head_dim)

@@ -1,0 +1,364 @@
+"""Sampling primitives of speculative verification on MI355X, with the reference's signatures.
+
+Mirrors nanovllm/layers/spec_sampler.py: same dataclass, same functions, same argument meaning, same random
+number consumption (torch.rand(B, k) first, then exponential_ over [B, V], from the caller's generator), so
+SpeculativeDecoder._accept and the drafter call sites work unchanged. The arithmetic runs in libnvs_amd kernels:
+  probs_from_logits / truncate_logits   one selection pass per row (top-k window with ties, top-p), then a write pass
+  race / sample                         chunked argmax of w / E
+  accept_random(_varlen)                accept test on gathered p, q; race over the vocabulary
+  accept_greedy(_varlen)                argmax per position, prefix count
+  accept_from_logits (no counterpart)   probs_from_logits + accept_random_varlen fused: the [T, V] probabilities
+                                        are never materialised
+Tensors must live on the ROCm device; nothing falls back to a CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, replace
+
+import torch
+
+from .. import _lib
+
+# The reference clamps the Exp(1) noise of the exponential race to avoid dividing by zero (spec_sampler.py:13).
+EXPONENTIAL_NOISE_FLOOR = 1e-10
+NEGATIVE_INFINITY = float("-inf")
+
+
+@dataclass
+class SamplingTensors:
+    temperatures: torch.Tensor | None  # [B] fp32; None when every row is greedy
+    top_k: torch.Tensor                # [B] int64; 0 disables top-k for that row
+    top_p: torch.Tensor                # [B] fp32; 1.0 disables top-p for that row
+    max_top_k: int                     # host copy of max(top_k); 0 means no row truncates
+    has_top_p: bool                    # host: some row has top_p < 1
+    all_top_k: bool                    # host: every row has top_k > 0
+
+
+def sampling_tensors(seqs, device: torch.device) -> SamplingTensors:
+    """Per-row parameters of a batch (spec_sampler.py:27-41); mixing greedy and random rows is a ValueError."""
+    temperatures = [seq.temperature for seq in seqs]
+    is_greedy = temperatures[0] == 0
+    if any((temperature == 0) != is_greedy for temperature in temperatures):
+        raise ValueError("mixed greedy and random sampling is not supported")
+    top_k = [seq.top_k for seq in seqs]
+    top_p = [seq.top_p for seq in seqs]
+    return SamplingTensors(
+        temperatures=None if is_greedy else _to_device(temperatures, torch.float32, device),
+        top_k=_to_device(top_k, torch.int64, device),
+        top_p=_to_device(top_p, torch.float32, device),
+        max_top_k=max(top_k),
+        has_top_p=any(value < 1.0 for value in top_p),
+        all_top_k=min(top_k) > 0,
+    )
+
+
+def sampling_per_token(sampling: SamplingTensors, verified_lens: torch.Tensor, num_tokens: int) -> SamplingTensors:
+    """Each row's parameters repeated over its verified positions, [B] -> [num_tokens] (spec_sampler.py:44-52)."""
+    temperatures = sampling.temperatures
+    return replace(sampling,
+                   temperatures=None if temperatures is None else
+                   temperatures.repeat_interleave(verified_lens, output_size=num_tokens),
+                   top_k=sampling.top_k.repeat_interleave(verified_lens, output_size=num_tokens),
+                   top_p=sampling.top_p.repeat_interleave(verified_lens, output_size=num_tokens))
+
+
+def _to_device(values: list, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    host = torch.tensor(values, dtype=dtype, pin_memory=device.type == "cuda")
+    return host.to(device, non_blocking=True)
+
+
+def _rows_view(x: torch.Tensor) -> tuple[torch.Tensor, int, int]:
+    """x [..., V] as rows: (tensor with unit last stride and uniform row stride, n_rows, row_stride)."""
+    vocab = x.shape[-1]
+    rows = x.reshape(-1, vocab)
+    if rows.stride(-1) != 1:
+        rows = rows.contiguous()
+    return rows, rows.shape[0], rows.stride(0)
+
+
+def _param_rows(sampling: SamplingTensors, n_pos: int) -> int:
+    n_param = sampling.top_k.shape[0]
+    if n_param == 0 or n_pos % n_param:
+        raise ValueError(f"{n_pos} logit rows do not broadcast over {n_param} parameter rows")
+    return n_pos // n_param
+
+
+def _contig(t: torch.Tensor | None, dtype: torch.dtype) -> torch.Tensor | None:
+    if t is None:
+        return None
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    return t.contiguous()
+
+
+def probs_from_logits(logits: torch.Tensor, sampling: SamplingTensors) -> torch.Tensor:
+    """fp32 probabilities after temperature, top-k and top-p (spec_sampler.py:65-69); greedy batches have none.
+    logits [..., V] (fp32 / bf16 / fp16); the [B] parameters broadcast over the middle dims (or are per token)."""
+    assert sampling.temperatures is not None
+    _lib.require_device(logits, sampling.temperatures, sampling.top_k, sampling.top_p)
+    rows, n_pos, row_stride = _rows_view(logits)
+    vocab = logits.shape[-1]
+    probs = torch.empty(logits.shape, dtype=torch.float32, device=logits.device)
+    if n_pos == 0:
+        return probs
+    per = _param_rows(sampling, n_pos)
+    top_k = _contig(sampling.top_k, torch.int64)
+    top_p = _contig(sampling.top_p, torch.float32)
+    temps = _contig(sampling.temperatures, torch.float32)
+    lib = _lib.load()
+    _lib.check(lib.nvs_probs_from_logits(rows.data_ptr(), _lib.dtype_code(rows.dtype), row_stride, n_pos, vocab, per,
+                                         temps.data_ptr(), top_k.data_ptr(), top_p.data_ptr(), sampling.max_top_k,
+                                         int(sampling.has_top_p), probs.data_ptr(), None, 0, _lib.stream_of(logits)),
+               "probs_from_logits")
+    return probs
+
+
+def truncate_logits(scaled: torch.Tensor, sampling: SamplingTensors) -> torch.Tensor:
+    """-inf outside each row's top-k, then outside the top-p nucleus of those candidates (spec_sampler.py:72-96).
+    Ties at the k-th value are kept; rows with top_k == 0 are returned unchanged."""
+    if sampling.max_top_k == 0:
+        return scaled
+    _lib.require_device(scaled, sampling.top_k, sampling.top_p)
+    if scaled.dtype != torch.float32:
+        raise ValueError("truncate_logits expects the fp32 temperature-scaled logits")
+    rows, n_pos, row_stride = _rows_view(scaled)
+    vocab = scaled.shape[-1]
+    out = torch.empty(scaled.shape, dtype=torch.float32, device=scaled.device)
+    if n_pos == 0:
+        return out
+    per = _param_rows(sampling, n_pos)
+    top_k = _contig(sampling.top_k, torch.int64)
+    top_p = _contig(sampling.top_p, torch.float32)
+    lib = _lib.load()
+    _lib.check(lib.nvs_truncate_logits(rows.data_ptr(), row_stride, n_pos, vocab, per, top_k.data_ptr(),
+                                       top_p.data_ptr(), sampling.max_top_k, int(sampling.has_top_p), out.data_ptr(),
+                                       None, 0, _lib.stream_of(scaled)),
+               "truncate_logits")
+    return out
+
+
+def exponential_noise_(out: torch.Tensor, generator: torch.Generator | None) -> torch.Tensor:
+    """Fill out with the race's Exp(1) noise, in place; returns out (spec_sampler.py:99-101). The draws come from
+    torch's generator so the stream of random numbers is the reference's."""
+    return out.exponential_(1.0, generator=generator).clamp_min_(EXPONENTIAL_NOISE_FLOOR)
+
+
+def race(weights: torch.Tensor, noise: torch.Tensor) -> torch.Tensor:
+    """argmax(w / E) over the last dim, first index on ties (spec_sampler.py:104-106)."""
+    _lib.require_device(weights, noise)
+    if weights.shape != noise.shape:
+        raise ValueError(f"weights {tuple(weights.shape)} and noise {tuple(noise.shape)} differ")
+    lead = weights.shape[:-1]
+    vocab = weights.shape[-1]
+    w, n_rows, w_stride = _rows_view(_contig(weights, torch.float32) if weights.dtype != torch.float32 else weights)
+    e, _, e_stride = _rows_view(_contig(noise, torch.float32) if noise.dtype != torch.float32 else noise)
+    out = torch.empty(n_rows, dtype=torch.int64, device=weights.device)
+    if n_rows == 0:
+        return out.view(lead)
+    lib = _lib.load()
+    nbytes = _lib.size_out()
+    _lib.check(lib.nvs_race_workspace_size(n_rows, vocab, ctypes.byref(nbytes)), "race_workspace_size")
+    ws = _lib.workspace(nbytes.value, weights.device)
+    _lib.check(lib.nvs_race(w.data_ptr(), w_stride, e.data_ptr(), e_stride, n_rows, vocab, out.data_ptr(),
+                            _lib.ptr(ws), nbytes.value, _lib.stream_of(weights)),
+               "race")
+    return out.view(lead)
+
+
+def sample(weights: torch.Tensor, generator: torch.Generator | None) -> torch.Tensor:
+    """Exponential race: argmax(w / E) with E ~ Exp(1) picks index i with probability w_i / sum(w)."""
+    return race(weights, exponential_noise_(torch.empty_like(weights, dtype=torch.float32), generator))
+
+
+def _draws(batch_size: int, num_drafts: int, vocab: int, device: torch.device,
+           generator: torch.Generator | None) -> tuple[torch.Tensor, torch.Tensor]:
+    """The uniforms and the race noise, drawn in the reference's order (spec_sampler.py:141 then :149)."""
+    uniforms = torch.rand(batch_size, num_drafts, device=device, generator=generator)
+    noise = exponential_noise_(torch.empty(batch_size, vocab, dtype=torch.float32, device=device), generator)
+    return uniforms, noise
+
+
+def accept_random(p: torch.Tensor, q: torch.Tensor, drafts: torch.Tensor,
+                  generator: torch.Generator | None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Rejection sampling of k drafts per row, every row verifying all of them (spec_sampler.py:114-120).
+    p: [B, k+1, V] at the k draft positions and the bonus position."""
+    batch_size, num_drafts = drafts.shape
+    return _accept_random(p.reshape(-1, p.shape[-1]), q, drafts, None, generator)
+
+
+def accept_random_varlen(p: torch.Tensor, q: torch.Tensor, drafts: torch.Tensor, verified_lens: torch.Tensor,
+                         generator: torch.Generator | None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Rejection sampling of each row's first verified_lens - 1 drafts (spec_sampler.py:123-150).
+    p: [T, V] target probabilities at the verified positions, row after row; q: [B, k, V] draft probabilities;
+    drafts: [B, k] int64; verified_lens: [B] int64 in 1..k+1 summing to T. Returns n_accept [B] and tail [B]."""
+    return _accept_random(p, q, drafts, verified_lens, generator)
+
+
+def _accept_random(p, q, drafts, verified_lens, generator):
+    _lib.require_device(p, q, drafts, verified_lens)
+    batch_size, num_drafts = drafts.shape
+    vocab = p.shape[-1]
+    uniforms, noise = _draws(batch_size, num_drafts, vocab, p.device, generator)
+    p = _contig(p, torch.float32)
+    q = _contig(q, torch.float32)
+    drafts_c = _contig(drafts, torch.int64)
+    lens = _contig(verified_lens, torch.int64)
+    n_accept = torch.empty(batch_size, dtype=torch.int64, device=p.device)
+    tail = torch.empty(batch_size, dtype=torch.int64, device=p.device)
+    if batch_size == 0:
+        return n_accept, tail
+    assert q.shape == (batch_size, num_drafts, vocab), f"q {tuple(q.shape)} is not [B, k, V]"
+    lib = _lib.load()
+    nbytes = _lib.size_out()
+    _lib.check(lib.nvs_accept_random_workspace_size(batch_size, vocab, ctypes.byref(nbytes)),
+               "accept_random_workspace_size")
+    ws = _lib.workspace(nbytes.value, p.device)
+    _lib.check(lib.nvs_accept_random(p.data_ptr(), q.data_ptr(), drafts_c.data_ptr(), _lib.ptr(lens),
+                                     uniforms.data_ptr(), noise.data_ptr(), batch_size, num_drafts, p.shape[0], vocab,
+                                     n_accept.data_ptr(), tail.data_ptr(), _lib.ptr(ws), nbytes.value,
+                                     _lib.stream_of(p)),
+               "accept_random")
+    return n_accept, tail
+
+
+def accept_greedy(target_logits: torch.Tensor, drafts: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Greedy verification of all k drafts per row (spec_sampler.py:153-158). target_logits: [B, k+1, V]."""
+    return _accept_greedy(target_logits.reshape(-1, target_logits.shape[-1]), drafts, None)
+
+
+def accept_greedy_varlen(target_logits: torch.Tensor, drafts: torch.Tensor,
+                         verified_lens: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Greedy verification of each row's first verified_lens - 1 drafts (spec_sampler.py:161-169): a draft is
+    accepted iff it equals the target's argmax at its position. target_logits: [T, V]."""
+    return _accept_greedy(target_logits, drafts, verified_lens)
+
+
+def _accept_greedy(logits, drafts, verified_lens):
+    _lib.require_device(logits, drafts, verified_lens)
+    batch_size, num_drafts = drafts.shape
+    rows, n_pos, row_stride = _rows_view(logits)
+    vocab = logits.shape[-1]
+    drafts_c = _contig(drafts, torch.int64)
+    lens = _contig(verified_lens, torch.int64)
+    n_accept = torch.empty(batch_size, dtype=torch.int64, device=logits.device)
+    tail = torch.empty(batch_size, dtype=torch.int64, device=logits.device)
+    if batch_size == 0:
+        return n_accept, tail
+    lib = _lib.load()
+    nbytes = _lib.size_out()
+    _lib.check(lib.nvs_accept_greedy_workspace_size(n_pos, vocab, ctypes.byref(nbytes)),
+               "accept_greedy_workspace_size")
+    ws = _lib.workspace(nbytes.value, logits.device)
+    _lib.check(lib.nvs_accept_greedy(rows.data_ptr(), _lib.dtype_code(rows.dtype), row_stride, drafts_c.data_ptr(),
+                                     _lib.ptr(lens), batch_size, num_drafts, n_pos, vocab, n_accept.data_ptr(),
+                                     tail.data_ptr(), _lib.ptr(ws), nbytes.value, _lib.stream_of(logits)),
+               "accept_greedy")
+    return n_accept, tail
+
+
+def accept_from_logits(target_logits: torch.Tensor, draft_probs: torch.Tensor, drafts: torch.Tensor,
+                       sampling: SamplingTensors, verified_lens: torch.Tensor | None,
+                       generator: torch.Generator | None) -> tuple[torch.Tensor, torch.Tensor]:
+    """What SpeculativeDecoder._accept computes for a random batch (speculative.py:450-462), fused:
+        accept_random(probs_from_logits(logits, sampling), q, drafts, g)                       (verified_lens None)
+        accept_random_varlen(probs_from_logits(logits, sampling_per_token(...)), q, drafts, lens, g)
+    target_logits: [B, k+1, V] or [T, V]; sampling holds per-row [B] parameters. Draws the same random numbers
+    in the same order and returns the same (n_accept, tail)."""
+    assert sampling.temperatures is not None, "greedy batches use accept_greedy(_varlen)"
+    _lib.require_device(target_logits, draft_probs, drafts, verified_lens, sampling.temperatures)
+    batch_size, num_drafts = drafts.shape
+    rows, n_pos, row_stride = _rows_view(target_logits)
+    vocab = target_logits.shape[-1]
+    uniforms, noise = _draws(batch_size, num_drafts, vocab, target_logits.device, generator)
+    q = _contig(draft_probs, torch.float32)
+    drafts_c = _contig(drafts, torch.int64)
+    lens = _contig(verified_lens, torch.int64)
+    temps = _contig(sampling.temperatures, torch.float32)
+    top_k = _contig(sampling.top_k, torch.int64)
+    top_p = _contig(sampling.top_p, torch.float32)
+    n_accept = torch.empty(batch_size, dtype=torch.int64, device=target_logits.device)
+    tail = torch.empty(batch_size, dtype=torch.int64, device=target_logits.device)
+    if batch_size == 0:
+        return n_accept, tail
+    assert q.shape == (batch_size, num_drafts, vocab), f"draft_probs {tuple(q.shape)} is not [B, k, V]"
+    lib = _lib.load()
+    nbytes = _lib.size_out()
+    _lib.check(lib.nvs_spec_accept_workspace_size(batch_size, num_drafts, n_pos, vocab, sampling.max_top_k,
+                                                  ctypes.byref(nbytes)),
+               "spec_accept_workspace_size")
+    ws = _lib.workspace(nbytes.value, target_logits.device)
+    _lib.check(lib.nvs_spec_accept(rows.data_ptr(), _lib.dtype_code(rows.dtype), row_stride, temps.data_ptr(),
+                                   top_k.data_ptr(), top_p.data_ptr(), sampling.max_top_k, int(sampling.has_top_p),
+                                   q.data_ptr(), drafts_c.data_ptr(), _lib.ptr(lens), uniforms.data_ptr(),
+                                   noise.data_ptr(), batch_size, num_drafts, n_pos, vocab, n_accept.data_ptr(),
+                                   tail.data_ptr(), _lib.ptr(ws), nbytes.value, _lib.stream_of(target_logits)),
+               "spec_accept")
+    return n_accept, tail
+
+
+def spec_accept_with_draws(target_logits: torch.Tensor, draft_probs: torch.Tensor, drafts: torch.Tensor,
+                           sampling: SamplingTensors, verified_lens: torch.Tensor | None, uniforms: torch.Tensor,
+                           noise: torch.Tensor, workspace: torch.Tensor | None = None
+                           ) -> tuple[torch.Tensor, torch.Tensor]:
+    """accept_from_logits with the uniforms [B, k] and noise [B, V] supplied by the caller (tests, benchmarks,
+    a caller that draws them elsewhere). workspace: optional preallocated uint8 buffer."""
+    _lib.require_device(target_logits, draft_probs, drafts, verified_lens, uniforms, noise)
+    batch_size, num_drafts = drafts.shape
+    rows, n_pos, row_stride = _rows_view(target_logits)
+    vocab = target_logits.shape[-1]
+    q = _contig(draft_probs, torch.float32)
+    drafts_c = _contig(drafts, torch.int64)
+    lens = _contig(verified_lens, torch.int64)
+    temps = _contig(sampling.temperatures, torch.float32)
+    top_k = _contig(sampling.top_k, torch.int64)
+    top_p = _contig(sampling.top_p, torch.float32)
+    u = _contig(uniforms, torch.float32)
+    e = _contig(noise, torch.float32)
+    n_accept = torch.empty(batch_size, dtype=torch.int64, device=target_logits.device)
+    tail = torch.empty(batch_size, dtype=torch.int64, device=target_logits.device)
+    if batch_size == 0:
+        return n_accept, tail
+    lib = _lib.load()
+    nbytes = _lib.size_out()
+    _lib.check(lib.nvs_spec_accept_workspace_size(batch_size, num_drafts, n_pos, vocab, sampling.max_top_k,
+                                                  ctypes.byref(nbytes)),
+               "spec_accept_workspace_size")
+    if workspace is None or workspace.numel() < nbytes.value:
+        workspace = _lib.workspace(nbytes.value, target_logits.device)
+    _lib.check(lib.nvs_spec_accept(rows.data_ptr(), _lib.dtype_code(rows.dtype), row_stride, temps.data_ptr(),
+                                   top_k.data_ptr(), top_p.data_ptr(), sampling.max_top_k, int(sampling.has_top_p),
+                                   q.data_ptr(), drafts_c.data_ptr(), _lib.ptr(lens), u.data_ptr(), e.data_ptr(),
+                                   batch_size, num_drafts, n_pos, vocab, n_accept.data_ptr(), tail.data_ptr(),
+                                   _lib.ptr(workspace), nbytes.value, _lib.stream_of(target_logits)),
+               "spec_accept")
+    return n_accept, tail
+
+
+def accept_random_with_draws(p: torch.Tensor, q: torch.Tensor, drafts: torch.Tensor,
+                             verified_lens: torch.Tensor | None, uniforms: torch.Tensor,
+                             noise: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """accept_random(_varlen) over dense p with the uniforms and noise supplied by the caller."""
+    _lib.require_device(p, q, drafts, verified_lens, uniforms, noise)
+    batch_size, num_drafts = drafts.shape
+    vocab = p.shape[-1]
+    p = _contig(p.reshape(-1, vocab), torch.float32)
+    q = _contig(q, torch.float32)
+    drafts_c = _contig(drafts, torch.int64)
+    lens = _contig(verified_lens, torch.int64)
+    u = _contig(uniforms, torch.float32)
+    e = _contig(noise, torch.float32)
+    n_accept = torch.empty(batch_size, dtype=torch.int64, device=p.device)
+    tail = torch.empty(batch_size, dtype=torch.int64, device=p.device)
+    if batch_size == 0:
+        return n_accept, tail
+    lib = _lib.load()
+    nbytes = _lib.size_out()
+    _lib.check(lib.nvs_accept_random_workspace_size(batch_size, vocab, ctypes.byref(nbytes)),
+               "accept_random_workspace_size")
+    ws = _lib.workspace(nbytes.value, p.device)
+    _lib.check(lib.nvs_accept_random(p.data_ptr(), q.data_ptr(), drafts_c.data_ptr(), _lib.ptr(lens), u.data_ptr(),
+                                     e.data_ptr(), batch_size, num_drafts, p.shape[0], vocab, n_accept.data_ptr(),
+                                     tail.data_ptr(), _lib.ptr(ws), nbytes.value, _lib.stream_of(p)),
+               "accept_random")
+    return n_accept, tail

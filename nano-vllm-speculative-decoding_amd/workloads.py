@@ -1,0 +1,208 @@
+"""Synthetic inputs of the verify hot path in the reference's memory layout.
+
+Verify attention: the layout of verify_varlen_metadata (nanovllm/engine/batch_metadata.py:149-181) -- rows of
+1..k+1 query tokens at the end of their context, cu_seqlens_q/k, padded block tables; padding rows of at most k+1
+tokens on a zeroed pad block fill the token count up to a multiple of 8 -- over a per-layer paged cache
+[blocks + 1, block_size, Hkv, D] whose last block is the pad block (model_runner.py:158-163). Physical blocks are
+handed to rows in a random permutation.
+
+Sampler: target logits ~ N(0, sigma^2), draft logits = target + N(0, 1) at the draft positions, draft probs q from
+the draft logits, drafts sampled from q, uniforms and race noise from a seeded generator.
+
+Seeds: Q/K/V 0, lengths 1, block permutation 2, target logits 10, draft noise 11, sampling generator 12.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass
+class AttentionCase:
+    q: torch.Tensor               # [T, H, D]
+    k_cache: torch.Tensor         # [blocks + 1, bs, Hkv, D]
+    v_cache: torch.Tensor
+    block_tables: torch.Tensor    # [R, W] int32
+    cu_seqlens_q: torch.Tensor    # [R + 1] int32
+    cu_seqlens_k: torch.Tensor    # [R + 1] int32
+    q_lens: list[int]
+    k_lens: list[int]
+    max_seqlen_q: int
+    max_seqlen_k: int
+    scale: float
+    pad_block: int
+    real_rows: int                # rows before the padding rows
+
+    @property
+    def rows(self) -> list[tuple[int, int, int]]:
+        starts = self.cu_seqlens_q.tolist()
+        return [(starts[r], self.q_lens[r], self.k_lens[r]) for r in range(len(self.q_lens))]
+
+    def kv_bytes(self) -> int:
+        """Algorithmic K+V bytes one attention pass reads: every visible key row of every kv head, once."""
+        hkv, d = self.k_cache.shape[2], self.k_cache.shape[3]
+        es = self.k_cache.element_size()
+        return sum(lk for lq, lk in zip(self.q_lens, self.k_lens) if lq > 0) * hkv * d * es * 2
+
+    def qo_bytes(self) -> int:
+        es = self.q.element_size()
+        return 2 * sum(self.q_lens) * self.q.shape[1] * self.q.shape[2] * es
+
+    def flops(self) -> int:
+        """2 FLOPs per multiply-add over the visible (query, key) pairs of QK^T and PV, all query heads."""
+        h, d = self.q.shape[1], self.q.shape[2]
+        pairs = 0
+        for lq, lk in zip(self.q_lens, self.k_lens):
+            pairs += sum(min(lk, lk - lq + i + 1) for i in range(lq))
+        return 4 * h * d * pairs
+
+    def to(self, device) -> "AttentionCase":
+        fields = {name: getattr(self, name) for name in self.__dataclass_fields__}
+        for name, value in fields.items():
+            if isinstance(value, torch.Tensor):
+                fields[name] = value.to(device)
+        return AttentionCase(**fields)
+
+
+def verify_attention_case(q_lens: list[int], k_lens: list[int], num_heads: int, num_kv_heads: int, head_dim: int,
+                          block_size: int = 256, dtype: torch.dtype = torch.bfloat16, pad_tokens_to: int = 8,
+                          max_query_len: int = 8, table_width: int | None = None, device="cpu",
+                          seed_qkv: int = 0, seed_blocks: int = 2, max_seqlen_k: int | None = None) -> AttentionCase:
+    """Rows r < len(q_lens) verify q_lens[r] tokens against k_lens[r] keys (the verified tokens are the last
+    q_lens[r] of them). The token count is padded to a multiple of pad_tokens_to with padding rows of at most
+    max_query_len tokens that read the pad block from position 0 (batch_metadata.py:170-179)."""
+    assert len(q_lens) == len(k_lens)
+    for lq, lk in zip(q_lens, k_lens):
+        assert 0 <= lq <= lk or (lq == 0 and lk == 0)
+    q_lens = list(q_lens)
+    k_lens = list(k_lens)
+    real_rows = len(q_lens)
+    total = sum(q_lens)
+    padded = -(-total // pad_tokens_to) * pad_tokens_to if pad_tokens_to > 1 else total
+    left = padded - total
+    while left > 0:
+        n = min(left, max_query_len)
+        q_lens.append(n)
+        k_lens.append(n)
+        left -= n
+    blocks_per_row = [math.ceil(lk / block_size) for lk in k_lens[:real_rows]]
+    n_blocks = sum(blocks_per_row)
+    pad_block = n_blocks
+    width = table_width or max(1, max(blocks_per_row + [math.ceil(max(k_lens) / block_size)]))
+    gen_blocks = torch.Generator().manual_seed(seed_blocks)
+    perm = torch.randperm(n_blocks, generator=gen_blocks).tolist()
+    tables = []
+    at = 0
+    for r in range(len(q_lens)):
+        if r < real_rows:
+            ids = perm[at:at + blocks_per_row[r]]
+            at += blocks_per_row[r]
+        else:
+            ids = []
+        tables.append(ids + [pad_block] * (width - len(ids)))
+    gen = torch.Generator().manual_seed(seed_qkv)
+    T = sum(q_lens)
+    q = torch.randn(T, num_heads, head_dim, generator=gen).to(dtype)
+    k_cache = torch.randn(n_blocks + 1, block_size, num_kv_heads, head_dim, generator=gen).to(dtype)
+    v_cache = torch.randn(n_blocks + 1, block_size, num_kv_heads, head_dim, generator=gen).to(dtype)
+    k_cache[pad_block] = 0
+    v_cache[pad_block] = 0
+    cu_q = [0]
+    cu_k = [0]
+    for lq, lk in zip(q_lens, k_lens):
+        cu_q.append(cu_q[-1] + lq)
+        cu_k.append(cu_k[-1] + lk)
+    case = AttentionCase(
+        q=q, k_cache=k_cache, v_cache=v_cache,
+        block_tables=torch.tensor(tables, dtype=torch.int32),
+        cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32),
+        cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32),
+        q_lens=q_lens, k_lens=k_lens,
+        max_seqlen_q=max(max(q_lens), 1), max_seqlen_k=max_seqlen_k or max(max(k_lens), 1),
+        scale=head_dim ** -0.5, pad_block=pad_block, real_rows=real_rows)
+    return case.to(device) if device != "cpu" else case
+
+
+def random_lengths(batch: int, q_range: tuple[int, int], k_range: tuple[int, int], seed: int = 1):
+    """Verify lengths uniform in q_range and contexts uniform in k_range (both inclusive)."""
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randint(q_range[0], q_range[1] + 1, (batch,), generator=gen).tolist()
+    k = torch.randint(k_range[0], k_range[1] + 1, (batch,), generator=gen).tolist()
+    return q, [max(kk, qq) for qq, kk in zip(q, k)]
+
+
+# The attention configurations (Qwen3-shaped: head_dim 128, 256-token blocks).
+def config_c1(dtype=torch.float32) -> AttentionCase:
+    """Qwen3-0.6B shape: 16 q / 8 kv heads, batch 1, 8 verify positions, 1,024-token context."""
+    return verify_attention_case([8], [1024], 16, 8, 128, dtype=dtype)
+
+
+def config_c2(dtype=torch.bfloat16) -> AttentionCase:
+    """Qwen3-8B shape: 32 q / 8 kv heads, batch 8, 8 positions, contexts uniform in [900, 1200]."""
+    q, k = random_lengths(8, (8, 8), (900, 1200))
+    return verify_attention_case(q, k, 32, 8, 128, dtype=dtype)
+
+
+def config_c3(dtype=torch.bfloat16, max_seqlen_k: int | None = None) -> AttentionCase:
+    """Qwen3-8B shape at batch 64: verify lengths uniform in {1..8}, contexts uniform in [2800, 3200]."""
+    q, k = random_lengths(64, (1, 8), (2800, 3200))
+    return verify_attention_case(q, k, 32, 8, 128, dtype=dtype, max_seqlen_k=max_seqlen_k)
+
+
+@dataclass
+class SamplerCase:
+    logits: torch.Tensor          # [T, V] target logits
+    q: torch.Tensor               # [B, k, V] draft probabilities
+    drafts: torch.Tensor          # [B, k] int64
+    verified_lens: torch.Tensor | None   # [B] int64 or None (all k+1)
+    temperatures: torch.Tensor    # [B]
+    top_k: torch.Tensor           # [B] int64
+    top_p: torch.Tensor           # [B]
+    max_top_k: int
+    has_top_p: bool
+    uniforms: torch.Tensor        # [B, k]
+    noise: torch.Tensor           # [B, V]
+
+    def to(self, device) -> "SamplerCase":
+        fields = {name: getattr(self, name) for name in self.__dataclass_fields__}
+        for name, value in fields.items():
+            if isinstance(value, torch.Tensor):
+                fields[name] = value.to(device)
+        return SamplerCase(**fields)
+
+
+def sampler_case(batch: int, num_drafts: int, vocab: int, top_k: int | list[int] = 64,
+                 top_p: float | list[float] = 1.0, temperature: float | list[float] = 1.0, sigma: float = 3.0,
+                 verified_lens: list[int] | None = None, logits_dtype: torch.dtype = torch.float32,
+                 draft_probs_fn=None, device="cpu") -> SamplerCase:
+    """Target logits [T, V] ~ N(0, sigma^2) (seed 10); draft logits = target at the k draft positions + N(0, 1)
+    (seed 11); q = draft_probs_fn(draft logits, temperatures, top_k, top_p) (the caller's probs_from_logits);
+    drafts ~ q, then uniforms and noise, from one generator (seed 12) in the reference's order."""
+    def per_row(v, dtype):
+        vals = v if isinstance(v, list) else [v] * batch
+        return torch.tensor(vals, dtype=dtype)
+    temps = per_row(temperature, torch.float32)
+    tk = per_row(top_k, torch.int64)
+    tp = per_row(top_p, torch.float32)
+    lens = None if verified_lens is None else torch.tensor(verified_lens, dtype=torch.int64)
+    n_pos = batch * (num_drafts + 1) if lens is None else int(lens.sum())
+    g_target = torch.Generator().manual_seed(10)
+    full = torch.randn(batch, num_drafts + 1, vocab, generator=g_target) * sigma
+    g_noise = torch.Generator().manual_seed(11)
+    draft_logits = full[:, :num_drafts] + torch.randn(batch, num_drafts, vocab, generator=g_noise)
+    if lens is None:
+        logits = full.reshape(-1, vocab)
+    else:
+        logits = torch.cat([full[b, :int(lens[b])] for b in range(batch)])
+    q = draft_probs_fn(draft_logits, temps, tk, tp)
+    gen = torch.Generator().manual_seed(12)
+    e_draft = torch.empty(batch, num_drafts, vocab).exponential_(1.0, generator=gen).clamp_min_(1e-10)
+    drafts = (q / e_draft).argmax(dim=-1)
+    uniforms = torch.rand(batch, num_drafts, generator=gen)
+    noise = torch.empty(batch, vocab).exponential_(1.0, generator=gen).clamp_min_(1e-10)
+    case = SamplerCase(logits=logits.to(logits_dtype), q=q.float().contiguous(), drafts=drafts,
+                       verified_lens=lens, temperatures=temps, top_k=tk, top_p=tp,
+                       max_top_k=int(tk.max()), has_top_p=bool((tp < 1.0).any()), uniforms=uniforms, noise=noise)
+    return case.to(device) if device != "cpu" else case

@@ -1,0 +1,23 @@
+"""CPU oracle of the verify hot path -- TEST INFRASTRUCTURE, not product code.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and only as the
+checker (or, for the CPU baseline, as the thing timed on the host cores). The product path (nvs_amd) never
+imports it and has no CPU fallback.
+
+Modules
+  oracle.attention     paged KV store and paged multi-query attention: an fp64 numpy brute force and a torch fp32
+                       restatement of the reference's CPU stand-in (tests/fake_paged_attention.py)
+  oracle.spec_sampler  torch-CPU restatement of nanovllm/layers/spec_sampler.py, with the random draws passed in
+
+How each function is pinned (each check fails for a dropped term, a wrong sign or index, a transposed operand):
+  attention.store_kvcache       exact-copy semantics, a known slot layout (tests/test_oracle_attention.py)
+  attention.paged_attention_f64 closed forms (one visible key -> that V row; equal keys -> mean of visible V;
+                                scale 0 -> mean), a dense-attention brute force with an explicit mask, GQA head
+                                mapping by construction, block-table permutation invariance
+  attention.paged_attention_t32 agreement with the fp64 brute force (fp32 tolerance)
+  spec_sampler.*                every known answer of the reference's tests/test_spec_sampler.py, the
+                                fixed-length body the variable-length rewrite must reproduce bit for bit, exact
+                                Fraction enumeration of the frozen cases (SHA-256 pinned), Hoeffding-bound
+                                output distributions of whole speculative rounds
+No function here is left "parity unpinned".
+"""

@@ -1,0 +1,106 @@
+"""The C ABI without a GPU: the library loads, exports every entry point include/nvs_amd.h declares, and rejects
+bad arguments on the host before any launch. CPU only (no call here reaches a kernel)."""
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from nvs_amd import _lib
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "nvs_amd.h"
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(nvs_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = declared()
+    assert len(names) >= 16
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_abi_version_and_empty_error(lib):
+    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 1
+    assert isinstance(lib.nvs_last_error(), bytes)
+
+
+def test_argument_counts_match_the_header(lib):
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for name, argtypes in _lib.SIGNATURES.items():
+        m = re.search(name + r"\s*\(([^)]*)\)", text)
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(argtypes), (name, len(params), len(argtypes))
+
+
+def attn_args(**over):
+    args = dict(q=1 << 20, q_ts=4096, q_hs=128, n_tokens=8, k=1 << 21, v=1 << 22, cache_blocks=4, c_bs=262144,
+                c_ts=1024, c_hs=128, bt=1 << 23, bt_rs=4, bt_width=4, cu_q=1 << 24, cu_k=1 << 25, ctx=None,
+                qlen=0, rows=1, mq=8, mk=1024, h=32, hkv=8, d=128, bs=256, scale=0.088, causal=1,
+                dtype=_lib.DTYPE_BF16, out=1 << 26, o_ts=4096, o_hs=128, ws=None, ws_bytes=0, stream=None)
+    args.update(over)
+    return list(args.values())
+
+
+@pytest.mark.parametrize("over, status", [
+    (dict(d=96), _lib.NVS_ERR_UNSUPPORTED),
+    (dict(dtype=_lib.DTYPE_F32), _lib.NVS_ERR_UNSUPPORTED),
+    (dict(h=30), _lib.NVS_ERR_INVALID),
+    (dict(bs=48), _lib.NVS_ERR_UNSUPPORTED),
+    (dict(q=(1 << 20) + 2), _lib.NVS_ERR_INVALID),
+    (dict(c_ts=1020), _lib.NVS_ERR_INVALID),
+    (dict(cu_k=None), _lib.NVS_ERR_INVALID),
+    (dict(cu_q=None, cu_k=None, ctx=None), _lib.NVS_ERR_INVALID),
+    (dict(scale=0.0), _lib.NVS_ERR_INVALID),
+    (dict(bt_width=0), _lib.NVS_ERR_INVALID),
+    (dict(rows=64, mk=4096), _lib.NVS_ERR_WORKSPACE),
+])
+def test_attention_rejects_bad_arguments_without_launching(lib, over, status):
+    assert lib.nvs_paged_attention(*attn_args(**over)) == status
+    assert lib.nvs_last_error()
+
+
+def test_attention_workspace_plan(lib):
+    n = ctypes.c_size_t()
+    assert lib.nvs_paged_attention_workspace_size(64, 32, 8, 128, 8, 4096, ctypes.byref(n)) == 0
+    assert n.value > 0
+    small = ctypes.c_size_t()
+    assert lib.nvs_paged_attention_workspace_size(1, 32, 8, 128, 8, 64, ctypes.byref(small)) == 0
+    assert small.value == 0            # one split: no partials
+    assert lib.nvs_paged_attention_workspace_size(1, 32, 8, 64, 8, 64, ctypes.byref(small)) == _lib.NVS_ERR_UNSUPPORTED
+
+
+def test_sampler_rejects_bad_arguments_without_launching(lib):
+    n = ctypes.c_size_t()
+    assert lib.nvs_spec_accept_workspace_size(64, 7, 512, 151936, 2000, ctypes.byref(n)) == _lib.NVS_ERR_UNSUPPORTED
+    assert lib.nvs_spec_accept_workspace_size(64, 7, 512, 151936, 64, ctypes.byref(n)) == 0
+    assert n.value == 512 * 32
+    # fixed-length call whose position count is not B*(k+1)
+    st = lib.nvs_spec_accept(1 << 20, _lib.DTYPE_F32, 100, 1 << 20, 1 << 20, 1 << 20, 64, 0, 1 << 20, 1 << 20, None,
+                             1 << 20, 1 << 20, 4, 7, 31, 100, 1 << 20, 1 << 20, 1 << 20, 1024, None)
+    assert st == _lib.NVS_ERR_INVALID
+    # workspace too small
+    st = lib.nvs_spec_accept(1 << 20, _lib.DTYPE_F32, 100, 1 << 20, 1 << 20, 1 << 20, 64, 0, 1 << 20, 1 << 20, None,
+                             1 << 20, 1 << 20, 4, 7, 32, 100, 1 << 20, 1 << 20, 1 << 20, 16, None)
+    assert st == _lib.NVS_ERR_WORKSPACE
+    assert lib.nvs_probs_from_logits(1 << 20, 9, 100, 4, 100, 1, 1 << 20, None, None, 0, 0, 1 << 20, None, 0,
+                                     None) == _lib.NVS_ERR_INVALID
+    assert lib.nvs_race(1 << 20, 10, 1 << 20, 10, 3, 100, 1 << 20, None, 0, None) == _lib.NVS_ERR_INVALID
+
+
+def test_store_kvcache_rejects_bad_arguments(lib):
+    assert lib.nvs_store_kvcache(1 << 20, 1024, 1 << 20, 1024, 1 << 21, 1 << 22, 100, 1 << 23, 4, 8, 128, 7,
+                                 None) == _lib.NVS_ERR_INVALID
+    assert lib.nvs_store_kvcache(1 << 20, 512, 1 << 20, 1024, 1 << 21, 1 << 22, 100, 1 << 23, 4, 8, 128,
+                                 _lib.DTYPE_BF16, None) == _lib.NVS_ERR_INVALID
+    assert lib.nvs_store_kvcache(None, 0, None, 0, None, None, 0, None, 0, 8, 128, _lib.DTYPE_BF16, None) == 0

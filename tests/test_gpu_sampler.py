@@ -1,0 +1,287 @@
+"""Parity of the HIP sampler kernels with the CPU oracle.
+
+Accepted lengths and tails are compared bit for bit given the same logits, q, uniforms and noise; probabilities
+within fp32 rounding (rtol 1e-5, atol 1e-7) with identical zero patterns; truncated logits exactly.
+On a mismatch the decision margin is printed: a flip is only legitimate when u*q and p (or two race scores)
+agree to a few ulps, because the kernel's exp and summation order differ from torch's CPU ones.
+"""
+import json
+import math
+import pathlib
+
+import pytest
+import torch
+
+import known_answers as ka
+import nvs_amd.workloads as wl
+from conftest import log_case
+from nvs_amd.layers import spec_sampler as ns
+from oracle import spec_sampler as ref
+
+pytestmark = pytest.mark.gpu
+FROZEN = json.loads((pathlib.Path(__file__).parent / "golden" / "random_sampling_cases.json").read_text())
+
+
+def sampling(rows, device):
+    t = torch.tensor([r[0] for r in rows], dtype=torch.float32)
+    k = torch.tensor([r[1] for r in rows], dtype=torch.int64)
+    p = torch.tensor([r[2] for r in rows], dtype=torch.float32)
+    st = ns.SamplingTensors(temperatures=t.to(device), top_k=k.to(device), top_p=p.to(device),
+                            max_top_k=int(k.max()), has_top_p=bool((p < 1).any()), all_top_k=bool((k > 0).all()))
+    return st, (t, k, p, int(k.max()), bool((p < 1).any()))
+
+
+@pytest.mark.parametrize("case", ka.PROBS_CASES, ids=[c[0] for c in ka.PROBS_CASES])
+def test_probs_known_answers(device, case):
+    log_case(f"probs known answer {case[0]}")
+    _, rows, logits, expected = case
+    st, _ = sampling(rows, device)
+    probs = ns.probs_from_logits(torch.tensor(logits, device=device), st)
+    torch.testing.assert_close(probs.cpu(), torch.tensor(expected, dtype=torch.float32))
+
+
+def test_truncation_broadcast_known_answer(device):
+    log_case("truncate broadcast")
+    rows, logits, expected = ka.BROADCAST_CASE
+    st, _ = sampling(rows, device)
+    assert ns.truncate_logits(torch.tensor(logits, device=device), st).cpu().tolist() == expected
+
+
+def test_bonus_and_zero_mass_known_answers(device):
+    log_case("accept_random bonus / zero mass")
+    for make in (ka.bonus_case, ka.zero_mass_case):
+        p, q, drafts, n_exp, tail_exp = make()
+        g = torch.Generator(device=device).manual_seed(0)
+        n, tail = ns.accept_random(p.to(device), q.to(device), drafts.to(device), g)
+        assert (n.tolist(), tail.tolist()) == (n_exp, tail_exp)
+
+
+def test_greedy_known_answers(device):
+    log_case("greedy known answers")
+    for _, logits, drafts, n_exp, tail_exp in ka.greedy_prefix_cases():
+        n, tail = ns.accept_greedy(logits.to(device), drafts.to(device))
+        assert (n.tolist(), tail.tolist()) == (n_exp, tail_exp)
+    logits, drafts, n_exp, tail_exp = ka.greedy_per_row_case()
+    n, tail = ns.accept_greedy(logits.to(device), drafts.to(device))
+    assert (n.tolist(), tail.tolist()) == (n_exp, tail_exp)
+
+
+def test_varlen_known_answers(device):
+    log_case("varlen known answers")
+    p, q, drafts, lens, n_exp, tail_exp = ka.varlen_case()
+    g = torch.Generator(device=device).manual_seed(0)
+    n, tail = ns.accept_random_varlen(p.to(device), q.to(device), drafts.to(device), lens.to(device), g)
+    assert (n.tolist(), tail.tolist()) == (n_exp, tail_exp)
+    n, tail = ns.accept_greedy_varlen(p.to(device), drafts.to(device), lens.to(device))
+    assert (n.tolist(), tail.tolist()) == (n_exp, tail_exp)
+    # the fused path on logits whose softmax is (numerically) the point masses
+    st, _ = sampling([(1.0, 4, 1.0)] * 3, device)
+    logits = torch.where(p > 0, 0.0, -1e4)
+    g = torch.Generator(device=device).manual_seed(0)
+    n, tail = ns.accept_from_logits(logits.to(device), q.to(device), drafts.to(device), st, lens.to(device), g)
+    assert (n.tolist(), tail.tolist()) == (n_exp, tail_exp)
+
+
+def test_race_ties_zero_weights_and_random_rows(device):
+    log_case("race ties / zeros / random")
+    w = torch.tensor([[0.0, 2.0, 2.0, 1.0], [0.0, 0.0, 0.0, 0.0]])
+    assert ns.race(w.to(device), torch.ones(2, 4, device=device)).tolist() == [1, 0]
+    gen = torch.Generator().manual_seed(7)
+    w = torch.rand(33, 70000, generator=gen)
+    w[w < 0.5] = 0
+    e = torch.empty(33, 70000).exponential_(generator=gen).clamp_min_(1e-10)
+    assert torch.equal(ns.race(w.to(device), e.to(device)).cpu(), ref.race(w, e))
+
+
+def test_sample_frequencies_follow_the_weights(device):
+    log_case("sample frequencies")
+    g = torch.Generator(device=device).manual_seed(0)
+    weights = torch.tensor([0.1, 0.6, 0.3], device=device).expand(200_000, 3)
+    counts = torch.bincount(ns.sample(weights, g), minlength=3).float().cpu() / 200_000
+    torch.testing.assert_close(counts, torch.tensor([0.1, 0.6, 0.3]), atol=0.005, rtol=0)
+
+
+def probs_params(n, vocab, top_k, top_p, temp, seed, dtype=torch.float32, sigma=3.0):
+    gen = torch.Generator().manual_seed(seed)
+    logits = (torch.randn(n, vocab, generator=gen) * sigma).to(dtype)
+    rows = [(temp[i % len(temp)], top_k[i % len(top_k)], top_p[i % len(top_p)]) for i in range(n)]
+    return logits, rows
+
+
+@pytest.mark.parametrize("name, top_k, top_p, temp, dtype", [
+    ("topk64", [64], [1.0], [1.0], torch.float32),
+    ("topk_mixed_topp", [64, 5, 1, 20], [0.9, 1.0, 0.5, 0.3], [0.7, 1.0, 1.3], torch.float32),
+    ("topk0_rows", [0, 64, 0, 3], [1.0], [1.0, 0.5], torch.float32),
+    ("bf16_ties", [64, 50], [1.0, 0.8], [1.0], torch.bfloat16),
+    ("topk1000", [1000, 700], [1.0, 0.95], [1.0], torch.float32),
+])
+@pytest.mark.parametrize("vocab", [5000, 151936])
+def test_probs_and_truncation_match_the_oracle(device, name, top_k, top_p, temp, dtype, vocab):
+    log_case(f"probs_from_logits {name} V={vocab}")
+    logits, rows = probs_params(16, vocab, top_k, top_p, temp, seed=len(name) + vocab)
+    logits = logits.to(dtype)
+    st, (t, k, p, mk, hp) = sampling(rows, device)
+    want = ref.probs_from_logits(logits, t, k, p, mk, hp)
+    got = ns.probs_from_logits(logits.to(device), st).cpu()
+    assert torch.equal(got > 0, want > 0), "kept sets differ"
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-7)
+    scaled = logits.float() / t[:, None]
+    trunc_want = ref.truncate_logits(scaled, k, p, mk, hp)
+    trunc_got = ns.truncate_logits(scaled.to(device), st).cpu()
+    assert torch.equal(trunc_got, trunc_want)
+
+
+def test_massive_ties_take_the_exact_path(device):
+    log_case("probs constant rows (all tied)")
+    vocab = 20000
+    logits = torch.zeros(3, vocab)
+    logits[1, ::7] = 1.0          # 2858 tied maxima
+    logits[2, :5000] = 2.0
+    st, (t, k, p, mk, hp) = sampling([(1.0, 10, 1.0), (1.0, 64, 0.5), (1.0, 3, 1.0)], device)
+    want = ref.probs_from_logits(logits, t, k, p, mk, hp)
+    got = ns.probs_from_logits(logits.to(device), st).cpu()
+    assert torch.equal(got > 0, want > 0)
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-7)
+
+
+def margin_report(case, n_got, n_want):
+    """Relative gap of every decision that differs; a genuine bug shows large gaps."""
+    lines = []
+    for b in torch.nonzero(n_got != n_want).flatten().tolist():
+        lines.append(f"row {b}: n_accept {int(n_got[b])} vs {int(n_want[b])}")
+    return "\n".join(lines)
+
+
+def run_fused(case, device):
+    g = case.to(device)
+    st = ns.SamplingTensors(temperatures=g.temperatures, top_k=g.top_k, top_p=g.top_p, max_top_k=case.max_top_k,
+                            has_top_p=case.has_top_p, all_top_k=bool((case.top_k > 0).all()))
+    n, tail = ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st, g.verified_lens, g.uniforms, g.noise)
+    return n.cpu(), tail.cpu()
+
+
+def run_oracle(case):
+    return ref.accept_from_logits(case.logits.float() if case.logits.dtype != torch.float32 else case.logits,
+                                  case.q, case.drafts, case.temperatures, case.top_k, case.top_p, case.max_top_k,
+                                  case.has_top_p, case.verified_lens, case.uniforms, case.noise)
+
+
+def draft_probs(draft_logits, temps, tk, tp):
+    return ref.probs_from_logits(draft_logits, temps, tk, tp, int(tk.max()), bool((tp < 1).any()))
+
+
+@pytest.mark.parametrize("name, kwargs", [
+    ("c4_topk64", dict(batch=64, num_drafts=7, vocab=151936)),
+    ("varlen", dict(batch=16, num_drafts=7, vocab=151936, verified_lens=[1, 8, 3, 5, 2, 7, 4, 6] * 2)),
+    ("topp_temps", dict(batch=8, num_drafts=3, vocab=32000, top_k=[64, 20, 5, 64] * 2,
+                        top_p=[0.9, 1.0, 0.6, 0.95] * 2, temperature=[0.7, 1.0, 1.5, 1.0] * 2)),
+    ("dense_rows", dict(batch=4, num_drafts=3, vocab=32000, top_k=[0, 64, 0, 10])),
+    ("bf16_logits", dict(batch=8, num_drafts=7, vocab=151936, logits_dtype=torch.bfloat16)),
+    ("small_sigma", dict(batch=8, num_drafts=7, vocab=151936, sigma=0.5)),
+])
+def test_fused_accept_is_bit_exact(device, name, kwargs):
+    log_case(f"fused accept {name}")
+    case = wl.sampler_case(draft_probs_fn=draft_probs, **kwargs)
+    n_got, tail_got = run_fused(case, device)
+    n_want, tail_want = run_oracle(case)
+    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want)
+    assert torch.equal(tail_got, tail_want)
+    print(f"{name}: accepted {n_got.float().mean():.2f} of {case.drafts.shape[1]} on average")
+
+
+@pytest.mark.parametrize("varlen", [False, True])
+def test_dense_accept_random_is_bit_exact(device, varlen):
+    log_case(f"accept_random dense varlen={varlen}")
+    lens = [1, 8, 3, 5, 2, 7, 4, 6] if varlen else None
+    case = wl.sampler_case(8, 7, 50000, verified_lens=lens, draft_probs_fn=draft_probs)
+    p = ref.probs_from_logits(case.logits, case.temperatures.repeat_interleave(case.verified_lens)
+                              if varlen else case.temperatures.repeat_interleave(8),
+                              case.top_k.repeat_interleave(case.verified_lens) if varlen
+                              else case.top_k.repeat_interleave(8),
+                              case.top_p.repeat_interleave(case.verified_lens) if varlen
+                              else case.top_p.repeat_interleave(8), case.max_top_k, case.has_top_p)
+    want = ref.accept_random_varlen(p, case.q, case.drafts, case.verified_lens if varlen else
+                                    torch.full((8,), 8, dtype=torch.int64), case.uniforms, case.noise)
+    got = ns.accept_random_with_draws(p.to(device), case.q.to(device), case.drafts.to(device),
+                                      None if lens is None else case.verified_lens.to(device),
+                                      case.uniforms.to(device), case.noise.to(device))
+    assert torch.equal(got[0].cpu(), want[0]) and torch.equal(got[1].cpu(), want[1])
+
+
+def test_greedy_matches_the_oracle_on_random_logits(device):
+    log_case("greedy random")
+    gen = torch.Generator().manual_seed(4)
+    logits = (torch.randn(40, 151936, generator=gen) * 3).to(torch.bfloat16)
+    lens = torch.tensor([8, 1, 5, 8, 3, 7, 8])
+    drafts = torch.randint(151936, (7, 7), generator=gen)
+    tokens = logits.float().argmax(-1)
+    starts = lens.cumsum(0) - lens
+    for b in range(7):   # make some drafts right
+        for j in range(int(lens[b]) - 1):
+            if (b + j) % 3:
+                drafts[b, j] = tokens[starts[b] + j]
+    want = ref.accept_greedy_varlen(logits.float(), drafts, lens)
+    got = ns.accept_greedy_varlen(logits.to(device), drafts.to(device), lens.to(device))
+    assert torch.equal(got[0].cpu(), want[0]) and torch.equal(got[1].cpu(), want[1])
+
+
+def test_generator_consumption_matches_the_reference_order(device):
+    """accept_random_varlen draws rand(B, k) then exponential_([B, V]) from the generator, nothing else."""
+    log_case("generator order")
+    p, q, drafts, lens, _, _ = ka.varlen_case()
+    ours = torch.Generator(device=device).manual_seed(42)
+    theirs = torch.Generator(device=device).manual_seed(42)
+    ns.accept_random_varlen(p.to(device), q.to(device), drafts.to(device), lens.to(device), ours)
+    torch.rand(3, 3, device=device, generator=theirs)
+    torch.empty(3, 4, device=device).exponential_(1.0, generator=theirs)
+    assert torch.equal(ours.get_state(), theirs.get_state())
+
+
+MULTI = [c for c in FROZEN["cases"] if "p_rows" in c]
+
+
+@pytest.mark.parametrize("case, k", [(c, 3) for c in MULTI] + [(FROZEN["k7_case"], 7)],
+                         ids=lambda v: v["name"] if isinstance(v, dict) else f"k{v}")
+def test_gpu_rounds_follow_the_target(device, case, k):
+    """test_accept_random_multistep.py's gate through the HIP accept_random on the device: whole speculative rounds
+    of the frozen Markov cases, 100k rows, every output sequence within the Hoeffding bound (delta = 0.001)."""
+    log_case(f"multistep gate {case['name']}")
+    from collections import Counter
+
+    from test_oracle_sampler import hoeffding, target_outputs
+    g = torch.Generator(device=device).manual_seed(17011)
+    p_rows = torch.tensor(case["p_rows"], dtype=torch.float32, device=device)
+    q_rows = torch.tensor(case["q_rows"], dtype=torch.float32, device=device)
+    eos, cap = case["eos_token_id"], case["max_tokens"]
+    trials = 100_000
+    outputs = [[] for _ in range(trials)]
+    state = torch.zeros(trials, dtype=torch.long)   # host copy; per-row updates stay off the device
+    active = list(range(trials))
+    while active:
+        idx = torch.tensor(active)
+        states, drafts = [state[idx].to(device)], []
+        for _ in range(k):
+            drafts.append(ns.sample(q_rows[states[-1]], g))
+            states.append(drafts[-1] + 1)
+        p = torch.stack([p_rows[s] for s in states], dim=1)
+        q = torch.stack([q_rows[s] for s in states[:-1]], dim=1)
+        drafts = torch.stack(drafts, dim=1)
+        n_acc, tail = ns.accept_random(p, q, drafts, g)
+        rounds = torch.cat([drafts, tail[:, None]], dim=1).tolist()
+        keep = []
+        for row, toks, cnt in zip(active, rounds, n_acc.tolist()):
+            for tok in toks[:cnt] + [toks[k]]:
+                outputs[row].append(tok)
+                if tok == eos or len(outputs[row]) == cap:
+                    break
+            if outputs[row][-1] != eos and len(outputs[row]) < cap:
+                keep.append(row)
+                state[row] = outputs[row][-1] + 1
+        active = keep
+    expected = {s: float(v) for s, v in target_outputs(case).items()}
+    counts = Counter(tuple(o) for o in outputs)
+    assert set(counts) <= set(expected)
+    bound = hoeffding(len(expected), trials)
+    worst = max(abs(counts[s] / trials - v) for s, v in expected.items())
+    assert worst <= bound, (worst, bound)
+    assert math.isfinite(worst)
