@@ -10,7 +10,7 @@
 #include <cstdio>
 #include <string>
 
-#include "../../include/nvs_amd.h"
+#include "nvs_amd.h"  // include/ is on the include path (build.py)
 
 namespace nvs {
 

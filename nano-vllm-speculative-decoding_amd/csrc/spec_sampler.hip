@@ -36,6 +36,9 @@ constexpr int kRaceChunk = 16384;              // vocabulary chunk of the dense 
 
 enum Mode { kModeAccept = 0, kModeProbs = 1, kModeTruncate = 2 };
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kFlagDense = 1;  // the race of this position must scan the whole vocabulary
 
 struct PosRecord {
@@ -322,7 +325,8 @@ __device__ __forceinline__ void load_vals(const void* row, int64_t e0, int64_t v
         for (int i = 0; i < kVpt / 4; ++i) {
             const int64_t e = e0 + (static_cast<int64_t>(i) * kSelThreads + threadIdx.x) * 4;
             if (vec && e + 4 <= vocab) {
-                const float4 x = *reinterpret_cast<const float4*>(p + e);
+                // streaming loads: each logit is read once per pass
+                const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + e));
                 v[4 * i] = x.x;
                 v[4 * i + 1] = x.y;
                 v[4 * i + 2] = x.z;
@@ -338,7 +342,7 @@ __device__ __forceinline__ void load_vals(const void* row, int64_t e0, int64_t v
         for (int i = 0; i < kVpt / 8; ++i) {
             const int64_t e = e0 + (static_cast<int64_t>(i) * kSelThreads + threadIdx.x) * 8;
             if (vec && e + 8 <= vocab) {
-                const uint4 x = *reinterpret_cast<const uint4*>(p + e);
+                const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + e));
                 const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
@@ -929,8 +933,8 @@ __device__ int64_t accepted_prefix(const RaceArgs& a, int64_t b, int64_t start, 
 template <bool kAccept>
 __global__ __launch_bounds__(256) void race_chunk_kernel(RaceArgs a) {
     __shared__ uint64_t red[4];
-    const int64_t r = blockIdx.y;
-    const int c = blockIdx.x;
+    const int64_t r = blockIdx.x;   // rows on x (up to 2^31), vocabulary chunks on y
+    const int c = blockIdx.y;
     const float* wrow;
     const float* qrow = nullptr;
     bool bonus = true;
@@ -941,6 +945,7 @@ __global__ __launch_bounds__(256) void race_chunk_kernel(RaceArgs a) {
         bonus = (n == L - 1);
         wrow = a.p + min(start + n, a.n_pos - 1) * a.p_stride;
         qrow = a.q + (r * a.k + (n < a.k - 1 ? n : a.k - 1)) * a.vocab;
+        if (c == 0 && threadIdx.x == 0) a.n_accept[r] = n;
     } else {
         wrow = a.p + r * a.p_stride;
     }
@@ -966,7 +971,7 @@ __global__ __launch_bounds__(256) void race_chunk_kernel(RaceArgs a) {
     }
 }
 
-template <bool kAccept>
+// Winner of each row over its chunk partials (the accepted prefix was written by the row's chunk 0).
 __global__ __launch_bounds__(64) void race_merge_kernel(RaceArgs a) {
     const int64_t r = blockIdx.x;
     uint64_t best = 0;
@@ -975,27 +980,7 @@ __global__ __launch_bounds__(64) void race_merge_kernel(RaceArgs a) {
         best = best > v ? best : v;
     }
     best = wave_max_u64(best);
-    int64_t n = 0;
-    if constexpr (kAccept) {
-        // recompute the prefix (k gathers) rather than carrying it between kernels
-        __shared__ int64_t start_sh;
-        if (threadIdx.x == 0) {
-            int64_t s = 0;
-            if (a.lens != nullptr) {
-                for (int64_t i = 0; i < r; ++i) s += a.lens[i];
-            } else {
-                s = r * (a.k + 1);
-            }
-            start_sh = s;
-        }
-        __syncthreads();
-        const int64_t L = a.lens != nullptr ? a.lens[r] : a.k + 1;
-        n = accepted_prefix(a, r, start_sh, L);
-    }
-    if (threadIdx.x == 0) {
-        a.out[r] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
-        if constexpr (kAccept) a.n_accept[r] = n;
-    }
+    if (threadIdx.x == 0) a.out[r] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
 }
 
 // ---------------------------------------------------------------- greedy
@@ -1032,17 +1017,14 @@ __global__ __launch_bounds__(kSelThreads) void argmax_kernel(const void* logits,
     }
 }
 
-__global__ __launch_bounds__(64) void greedy_finalize_kernel(const int64_t* tokens, const int64_t* drafts,
-                                                             const int64_t* lens, int64_t batch, int64_t n_pos,
-                                                             int k, int64_t* n_accept, int64_t* tail) {
-    const int64_t b = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
-    if (b >= batch) return;
-    int64_t start = 0;
-    if (lens != nullptr) {
-        for (int64_t i = 0; i < b; ++i) start += lens[i];
-    } else {
-        start = b * (k + 1);
-    }
+// One workgroup per batch row: the row's first position (a reduction over the lengths before it), then the
+// accepted prefix and the token after it.
+__global__ __launch_bounds__(256) void greedy_finalize_kernel(const int64_t* tokens, const int64_t* drafts,
+                                                              const int64_t* lens, int64_t batch, int64_t n_pos,
+                                                              int k, int64_t* n_accept, int64_t* tail) {
+    const int64_t b = blockIdx.x;
+    const int64_t start = row_start(lens, b, k);
+    if (threadIdx.x != 0) return;
     const int64_t L = lens != nullptr ? lens[b] : k + 1;
     int64_t n = 0;
     while (n < L - 1 && n < k && start + n < n_pos && tokens[start + n] == drafts[b * k + n]) ++n;
@@ -1176,10 +1158,13 @@ extern "C" int nvs_race(const float* weights, int64_t weights_row_stride, const 
                         size_t workspace_bytes, void* stream) {
     nvs::clear_error();
     NVS_CHECK(n_rows >= 0 && vocab > 0 && vocab < 0x7fffffffLL, NVS_ERR_INVALID, "race: bad sizes");
-    NVS_CHECK(n_rows <= 65535, NVS_ERR_UNSUPPORTED, "race: more than 65535 rows");
+    NVS_CHECK(n_rows <= 0x7fffffffLL, NVS_ERR_UNSUPPORTED, "race: too many rows");
     if (n_rows == 0) return NVS_OK;
     NVS_CHECK(weights && noise && out, NVS_ERR_INVALID, "race: null pointer");
-    NVS_CHECK(weights_row_stride >= vocab && noise_row_stride >= vocab, NVS_ERR_INVALID, "race: bad row strides");
+    // stride 0 = one row broadcast over all rows (an expanded tensor)
+    NVS_CHECK((weights_row_stride == 0 || weights_row_stride >= vocab) &&
+                  (noise_row_stride == 0 || noise_row_stride >= vocab),
+              NVS_ERR_INVALID, "race: bad row strides");
     size_t need = 0;
     nvs_race_workspace_size(n_rows, vocab, &need);
     NVS_CHECK(workspace != nullptr && workspace_bytes >= need, NVS_ERR_WORKSPACE,
@@ -1195,10 +1180,10 @@ extern "C" int nvs_race(const float* weights, int64_t weights_row_stride, const 
     a.partial = static_cast<uint64_t*>(workspace);
     a.out = out;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(race_chunk_kernel<false>, dim3(a.n_chunks, n_rows), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(race_chunk_kernel<false>, dim3(n_rows, a.n_chunks), dim3(256), 0, s, a);
     int st = nvs::check_launch("race chunk kernel");
     if (st != NVS_OK) return st;
-    hipLaunchKernelGGL(race_merge_kernel<false>, dim3(n_rows), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(race_merge_kernel, dim3(n_rows), dim3(64), 0, s, a);
     return nvs::check_launch("race merge kernel");
 }
 
@@ -1211,7 +1196,7 @@ static int accept_common_checks(const int64_t* drafts, int64_t batch, int num_dr
     NVS_CHECK(batch >= 0 && num_drafts >= 1 && n_pos >= 0 && vocab > 0, NVS_ERR_INVALID,
               "accept: bad sizes batch=%lld k=%d n_pos=%lld vocab=%lld", (long long)batch, num_drafts,
               (long long)n_pos, (long long)vocab);
-    NVS_CHECK(vocab < 0x7fffffffLL && batch <= 65535, NVS_ERR_UNSUPPORTED, "accept: sizes too large");
+    NVS_CHECK(vocab < 0x7fffffffLL && batch <= 0x7fffffffLL, NVS_ERR_UNSUPPORTED, "accept: sizes too large");
     NVS_CHECK(batch == 0 || (drafts && n_accept && tail), NVS_ERR_INVALID, "accept: null pointer");
     return NVS_OK;
 }
@@ -1250,10 +1235,10 @@ extern "C" int nvs_accept_random(const float* p, const float* q, const int64_t* 
     a.n_accept = n_accept;
     a.out = tail;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(race_chunk_kernel<true>, dim3(a.n_chunks, batch), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(race_chunk_kernel<true>, dim3(batch, a.n_chunks), dim3(256), 0, s, a);
     st = nvs::check_launch("accept_random chunk kernel");
     if (st != NVS_OK) return st;
-    hipLaunchKernelGGL(race_merge_kernel<true>, dim3(batch), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(race_merge_kernel, dim3(batch), dim3(64), 0, s, a);
     return nvs::check_launch("accept_random merge kernel");
 }
 
@@ -1293,7 +1278,7 @@ extern "C" int nvs_accept_greedy(const void* logits, int logits_dtype, int64_t l
     }
     st = nvs::check_launch("accept_greedy argmax kernel");
     if (st != NVS_OK) return st;
-    hipLaunchKernelGGL(greedy_finalize_kernel, dim3(static_cast<unsigned>((batch + 63) / 64)), dim3(64), 0, s, tokens,
+    hipLaunchKernelGGL(greedy_finalize_kernel, dim3(static_cast<unsigned>(batch)), dim3(256), 0, s, tokens,
                        drafts, verified_lens, batch, n_pos, num_drafts, n_accept, tail);
     return nvs::check_launch("accept_greedy finalize kernel");
 }

@@ -65,7 +65,7 @@ def paged_attention_f64(q, k_cache, v_cache, block_tables, rows, scale: float, c
         kq = keys[:, heads]                            # [Lk, H, D]
         vq = vals[:, heads]
         qr = q[q0:q0 + lq]                             # [Lq, H, D]
-        scores = np.einsum("ihd,jhd->hij", qr, kq) * scale   # [H, Lq, Lk]
+        scores = np.einsum("ihd,jhd->hij", qr, kq, optimize=True) * scale   # [H, Lq, Lk]
         j = np.arange(lk)[None, :]
         i = np.arange(lq)[:, None]
         visible = (j <= lk - lq + i) if causal else np.ones((lq, lk), dtype=bool)
@@ -75,7 +75,7 @@ def paged_attention_f64(q, k_cache, v_cache, block_tables, rows, scale: float, c
         w = np.exp(scores - m)
         z = w.sum(axis=-1, keepdims=True)
         p = np.divide(w, z, out=np.zeros_like(w), where=z > 0)
-        result[q0:q0 + lq] = np.einsum("hij,jhd->ihd", p, vq)
+        result[q0:q0 + lq] = np.einsum("hij,jhd->ihd", p, vq, optimize=True)
     return result
 
 

@@ -136,7 +136,7 @@ def accept_from_logits(logits: torch.Tensor, q: torch.Tensor, drafts: torch.Tens
     parameters, repeated over each row's verified positions like sampling_per_token (spec_sampler.py:44-52)."""
     batch, k = drafts.shape
     if verified_lens is None:
-        p = probs_from_logits(logits, temperatures, top_k, top_p, max_top_k, has_top_p)
+        p = probs_from_logits(logits.reshape(batch, k + 1, -1), temperatures, top_k, top_p, max_top_k, has_top_p)
         return accept_random(p, q, drafts, uniforms, noise)
     n_pos = logits.shape[0]
     per_token = [x.repeat_interleave(verified_lens, output_size=n_pos) for x in (temperatures, top_k, top_p)]
