@@ -117,7 +117,7 @@ def sampler_bench(args, dev):
     case = wl.sampler_case(64, 7, 151936, draft_probs_fn=draft_probs)
     g = case.to(dev)
     st = ns.SamplingTensors(g.temperatures, g.top_k, g.top_p, case.max_top_k, case.has_top_p, True)
-    ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)  # counters start at zero
 
     def step():
         ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st, None, g.uniforms, g.noise, workspace=ws)

@@ -160,7 +160,12 @@ int nvs_accept_greedy(const void* logits, int logits_dtype, int64_t logits_row_s
  * window plus ties, then top-p) is selected on chip, the accept test reads p and q at the draft token only, and
  * the residual max(p - q, 0) or bonus race reads q and the noise only inside the kept set (a row with top_k = 0
  * falls back to a full-vocabulary race). Same outputs as the two calls given the same uniforms and noise.
- * Sampling parameters are per batch row [B] (not per token). */
+ * Sampling parameters are per batch row [B] (not per token). verified_lens must sum to n_pos, as the reference
+ * requires (spec_sampler.py:127-129).
+ * One launch: the last position of each batch row to finish counts the row's accepted prefix and writes its
+ * outputs. row_counters: int32 [batch] device buffer that is zero on entry; every call leaves it zero again, so a
+ * caller keeps one zero-filled buffer and reuses it (calls sharing it must be ordered on one stream).
+ * workspace: scratch of nvs_spec_accept_workspace_size bytes, no initialisation needed. */
 int nvs_spec_accept_workspace_size(int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab, int max_top_k,
                                    size_t* bytes);
 int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_stride,
@@ -169,7 +174,8 @@ int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_str
                     const float* q, const int64_t* drafts, const int64_t* verified_lens,
                     const float* uniforms, const float* noise,
                     int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
-                    int64_t* n_accept, int64_t* tail, void* workspace, size_t workspace_bytes, void* stream);
+                    int64_t* n_accept, int64_t* tail, int32_t* row_counters,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -51,7 +51,7 @@ SIGNATURES = {
     "nvs_accept_greedy": [_p, _i32, _i64, _p, _p, _i64, _i32, _i64, _i64, _p, _p, _p, ctypes.c_size_t, _p],
     "nvs_spec_accept_workspace_size": [_i64, _i32, _i64, _i64, _i32, _size_p],
     "nvs_spec_accept": [_p, _i32, _i64, _p, _p, _p, _i32, _i32, _p, _p, _p, _p, _p, _i64, _i32, _i64, _i64, _p, _p,
-                        _p, ctypes.c_size_t, _p],
+                        _p, _p, ctypes.c_size_t, _p],
 }
 
 _lock = threading.Lock()
@@ -129,3 +129,21 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
     if nbytes == 0:
         return None
     return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+_persistent: dict = {}
+
+
+def persistent_workspace(name: str, nbytes: int, device: torch.device) -> torch.Tensor:
+    """A zero-initialised device buffer kept across calls, for kernels that keep counters in it and leave them at
+    zero when they finish (the fused accept's row counters). One buffer per (name, device); calls that share it
+    must be ordered on one stream. It is created outside graph capture: warm up once eagerly before capturing."""
+    key = (name, device.type, device.index)
+    buf = _persistent.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"nvs_amd: the {name} workspace must be created before graph capture; "
+                               "run the op once eagerly first")
+        buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _persistent[key] = buf
+    return buf

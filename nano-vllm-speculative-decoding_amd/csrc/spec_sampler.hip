@@ -31,6 +31,7 @@ constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kVpt = 16;                       // values per thread per batch
 constexpr int kBatch = kSelThreads * kVpt;     // 8192 elements per batch
 constexpr int kCap = 4096;                     // LDS candidate capacity
+constexpr int kWaveCap = kCap / kSelWaves;     // per-wave share of it during the streaming pass
 constexpr int kMaxTopK = 1024;
 constexpr int kRaceChunk = 16384;              // vocabulary chunk of the dense race kernels
 
@@ -72,6 +73,9 @@ struct SelArgs {
     int64_t batch;
     int k;
     PosRecord* rec;
+    int* counters;        // [batch] finished positions per row; zero between calls
+    int64_t* n_accept;
+    int64_t* tail;
     // dense outputs
     float* out;
     int64_t out_stride;
@@ -149,10 +153,15 @@ struct SelShared {
     float fred[kSelWaves];
     uint32_t ured[kSelWaves];
     uint64_t u64red[kSelWaves];
+    int wcount[kSelWaves];
     int count;
     int overflow;
+    int found;       // the position belongs to a batch row (fused accept)
+    int last;        // this workgroup finishes its batch row (fused accept)
     uint32_t sel_digit, sel_remaining, sel_greater, sel_equal;
     int64_t loc[4];  // b, j, L, start
+    int64_t fin_n;
+    PosRecord fin_rec;
 };
 
 // Sum over the workgroup (every thread gets the result).
@@ -285,6 +294,7 @@ __device__ void locate(const SelArgs& a, int64_t t, SelShared& sh) {
             sh.loc[1] = t % L;
             sh.loc[2] = L;
             sh.loc[3] = (t / L) * L;
+            sh.found = (t / L) < a.batch;
         }
         __syncthreads();
         return;
@@ -310,6 +320,7 @@ __device__ void locate(const SelArgs& a, int64_t t, SelShared& sh) {
             sh.loc[1] = t - start;
             sh.loc[2] = L;
             sh.loc[3] = start;
+            sh.found = 1;
         }
         carry += total;
     }
@@ -410,41 +421,6 @@ __device__ __forceinline__ void append_candidates(SelShared& sh, const uint32_t 
         }
         run += __popcll(bal[vi]);
     }
-}
-
-// Keep only candidates with key >= tau_key (order not preserved). Count must be <= kCap.
-__device__ void compact_candidates(SelShared& sh, uint32_t tau_key) {
-    constexpr int kPer = kCap / kSelThreads;
-    uint32_t k[kPer];
-    int32_t ix[kPer];
-    const int n = min(sh.count, kCap);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int c = threadIdx.x + i * kSelThreads;
-        k[i] = c < n ? sh.ckey[c] : 0u;
-        ix[i] = c < n ? sh.cidx[c] : 0;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) sh.count = 0;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const bool keep = k[i] != 0u && k[i] >= tau_key;
-        const uint64_t bal = __ballot(keep);
-        const int cnt = __popcll(bal);
-        if (cnt == 0) continue;
-        int base = 0;
-        if (lane_id() == 0) base = atomicAdd(&sh.count, cnt);
-        base = __shfl(base, 0);
-        const uint64_t below = (lane_id() == 0) ? 0ull : (~0ull >> (64 - lane_id()));
-        if (keep) {
-            const int pos = base + __popcll(bal & below);
-            sh.ckey[pos] = k[i];
-            sh.cidx[pos] = ix[i];
-        }
-    }
-    __syncthreads();
 }
 
 // Threshold of truncate_logits (spec_sampler.py:72-96) from the sorted top `rank` keys in sh.sortbuf:
@@ -582,6 +558,53 @@ __device__ RowStats exact_row_stats(const SelArgs& a, const void* row, bool vec,
     return rs;
 }
 
+// Finish batch row b of the fused accept (run by the workgroup whose position arrived last): the accepted prefix
+// n from the positions' decisions, then the tail = the race of position start + n, which that position already ran
+// over its kept set, or, for a row that does not truncate, a race over the whole vocabulary run here.
+template <int DT>
+__device__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L, SelShared& sh) {
+    const int kd = a.k;
+    if (threadIdx.x == 0) {
+        __threadfence();  // acquire: the other positions' records
+        int64_t n = 0;
+        while (n < L - 1 && n < kd && start + n < a.n_pos && a.rec[start + n].acc) ++n;
+        sh.fin_n = n;
+        sh.fin_rec = a.rec[min(start + n, a.n_pos - 1)];
+    }
+    __syncthreads();
+    const int64_t n = sh.fin_n;
+    const PosRecord r = sh.fin_rec;
+    int64_t winner = r.race;
+    if (r.flags & kFlagDense) {
+        const int64_t pos = min(start + n, a.n_pos - 1);
+        const bool bonus = (n == L - 1);
+        const int64_t qn = n < kd - 1 ? n : kd - 1;
+        const float* qrow = a.q + (b * kd + qn) * a.vocab;
+        const float* erow = a.noise + b * a.vocab;
+        const char* row = static_cast<const char*>(a.logits) + pos * a.row_stride * nvs::dtype_size(DT);
+        const uint32_t theta_key = r.theta == -INFINITY ? 0u : nvs::float_key(r.theta);
+        const float mu = (r.m == -INFINITY) ? 0.f : r.m;
+        const bool unit_temp = (r.temp == 1.f);
+        uint64_t best = 0;
+        for (int64_t i = threadIdx.x; i < a.vocab; i += blockDim.x) {
+            const float sc = scale_logit(nvs::load_as_float<DT>(row, i), r.temp, unit_temp);
+            const float p = (sel_key(sc) >= theta_key && sc == sc) ? expf(sc - mu) / r.z : 0.f;
+            const float w = bonus ? p : fmaxf(p - qrow[i], 0.f);
+            const float score = w / erow[i];
+            const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+                                 static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
+            best = best > k64 ? best : k64;
+        }
+        best = block_max_u64(best, sh);
+        winner = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
+    }
+    if (threadIdx.x == 0) {
+        a.n_accept[b] = n;
+        a.tail[b] = winner;
+        a.counters[b] = 0;  // ready for the next call
+    }
+}
+
 template <int DT, int MODE>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
     __shared__ SelShared sh;
@@ -589,6 +612,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
     if (threadIdx.x == 0) {
         sh.count = 0;
         sh.overflow = 0;
+        sh.found = 0;
+        sh.last = 0;
         sh.loc[0] = sh.loc[1] = sh.loc[3] = 0;
         sh.loc[2] = 1;
     }
@@ -638,64 +663,97 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
         rs.z = block_sum(zz, sh);
         rs.m = mall;
     } else {
-        // ---- one pass: candidate list of everything >= a lower bound of the K-th largest
-        uint32_t tau_key = 0u;
+        // ---- one pass: every element >= tau, a lower bound of the K-th largest, joins its wave's candidate list.
+        // tau comes from the first batch: each wave's ceil(K/8)-th largest lane maximum, the smallest over the 8
+        // waves, so at least K elements lie at or above it. After that the pass has no workgroup barrier: a wave
+        // appends to its own list, and a list that overflows sends the row to the exact path.
+        const int wave = threadIdx.x >> 6;
+        uint32_t* wkey = sh.ckey + wave * kWaveCap;
+        int32_t* widx = sh.cidx + wave * kWaveCap;
+        const uint64_t below = (lane_id() == 0) ? 0ull : (~0ull >> (64 - lane_id()));
+        float tau = INFINITY;
+        int wcount = 0;
         float vcur[kVpt];
         load_vals<DT>(row, 0, a.vocab, vec, vcur);
         for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
             float vnext[kVpt];
             const bool more = e0 + kBatch < a.vocab;
             if (more) load_vals<DT>(row, e0 + kBatch, a.vocab, vec, vnext);
-            uint32_t keys[kVpt];
+            float sv[kVpt];
 #pragma unroll
-            for (int vi = 0; vi < kVpt; ++vi) keys[vi] = sel_key(scale_logit(vcur[vi], temp, unit_temp));
+            for (int vi = 0; vi < kVpt; ++vi) sv[vi] = scale_logit(vcur[vi], temp, unit_temp);
             if (e0 == 0) {
-                // initial bound: each wave's ceil(K/8)-th largest lane maximum, smallest over the waves
                 uint32_t tmax = 0u;
 #pragma unroll
-                for (int vi = 0; vi < kVpt; ++vi) tmax = max(tmax, keys[vi]);
+                for (int vi = 0; vi < kVpt; ++vi) tmax = max(tmax, sel_key(sv[vi]));
                 const int rw = (K + kSelWaves - 1) / kSelWaves;
                 uint32_t bound = 0u;
                 if (rw <= 64) {
                     const uint32_t sorted = wave_sort_desc(tmax);
                     bound = static_cast<uint32_t>(__shfl(static_cast<int>(sorted), rw - 1));
                 }
-                if (lane_id() == 0) sh.ured[threadIdx.x >> 6] = bound;
+                if (lane_id() == 0) sh.ured[wave] = bound;
                 __syncthreads();
                 uint32_t b = 0xffffffffu;
                 for (int w = 0; w < kSelWaves; ++w) b = min(b, sh.ured[w]);
-                tau_key = b;
-                __syncthreads();
+                tau = (b == 0u) ? -INFINITY : nvs::key_float(b);   // NaN never passes a >= test
             }
-            append_candidates<DT>(sh, keys, e0, tau_key);
-            __syncthreads();
-            const int cnt = sh.count;
-            const int ovf = sh.overflow;
-            __syncthreads();  // everyone has read the count before the next batch appends
-            if (ovf) break;
-            if (cnt > kCap / 2) {
-                // prune to the exact K-th largest of the list
-                const int n = sh.count;
-                auto each = [&](auto&& fn) {
-                    for (int c = threadIdx.x; c < n; c += blockDim.x) fn(sh.ckey[c]);
-                };
-                uint32_t ng, ne;
-                const uint32_t kth = radix_select(each, static_cast<uint32_t>(K), sh, &ng, &ne);
-                tau_key = max(tau_key, kth);
-                compact_candidates(sh, tau_key);
-                const int kept = sh.count;
-                __syncthreads();
-                if (kept > kCap / 2) {
-                    // more than half the list is tied at the bound: let the exact path handle the row
-                    if (threadIdx.x == 0) sh.overflow = 1;
-                    __syncthreads();
-                    break;
+            bool any = false;
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) any |= (sv[vi] >= tau);
+            if (__ballot(any) != 0ull) {
+#pragma unroll
+                for (int vi = 0; vi < kVpt; ++vi) {
+                    const bool pass = sv[vi] >= tau;
+                    const uint64_t bal = __ballot(pass);
+                    if (pass) {
+                        const int pos = wcount + __popcll(bal & below);
+                        if (pos < kWaveCap) {
+                            wkey[pos] = nvs::float_key(sv[vi]);
+                            widx[pos] = static_cast<int32_t>(val_index<DT>(e0, vi));
+                        }
+                    }
+                    wcount += __popcll(bal);
                 }
+                if (wcount > kWaveCap) break;   // overflow: the exact path re-reads the row
             }
             if (more) {
 #pragma unroll
                 for (int vi = 0; vi < kVpt; ++vi) vcur[vi] = vnext[vi];
             }
+        }
+        if (lane_id() == 0) {
+            sh.wcount[wave] = min(wcount, kWaveCap);
+            if (wcount > kWaveCap) sh.overflow = 1;
+        }
+        __syncthreads();
+        if (!sh.overflow) {
+            // the per-wave lists, one after another
+            int off = 0, total = 0;
+            for (int w = 0; w < kSelWaves; ++w) {
+                off += (w < wave) ? sh.wcount[w] : 0;
+                total += sh.wcount[w];
+            }
+            const int cnt = sh.wcount[wave];
+            constexpr int kPer = kWaveCap / 64;
+            uint32_t kk[kPer];
+            int32_t ii[kPer];
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                const int c = lane_id() + 64 * j;
+                kk[j] = c < cnt ? wkey[c] : 0u;
+                ii[j] = c < cnt ? widx[c] : 0;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                const int c = lane_id() + 64 * j;
+                if (c < cnt) {
+                    sh.ckey[off + c] = kk[j];
+                    sh.cidx[off + c] = ii[j];
+                }
+            }
+            if (threadIdx.x == 0) sh.count = total;
         }
         __syncthreads();
         if (sh.overflow) {
@@ -807,27 +865,18 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
             }
             r.race = winner;
             a.rec[t] = r;
+            // release this record, then count the position; the row's last position to arrive finishes the row
+            __threadfence();
+            if (sh.found) {
+                const int64_t L_eff = min(max(L, int64_t{1}), static_cast<int64_t>(kd) + 1);
+                sh.last = (atomicAdd(&a.counters[b], 1) == static_cast<int>(L_eff) - 1);
+            }
         }
+        __syncthreads();
+        if (!sh.last) return;
+        finish_row<DT>(a, b, sh.loc[3], L, sh);
     }
 }
-
-// ---------------------------------------------------------------- fused accept: finalize per batch row
-
-struct FinArgs {
-    const void* logits;
-    int64_t row_stride;
-    int64_t vocab;
-    const float* q;
-    const int64_t* drafts;
-    const int64_t* lens;
-    const float* noise;
-    int64_t batch;
-    int64_t n_pos;
-    int k;
-    const PosRecord* rec;
-    int64_t* n_accept;
-    int64_t* tail;
-};
 
 __device__ __forceinline__ int64_t row_start(const int64_t* lens, int64_t b, int k) {
     // exclusive prefix of lens over rows < b (workgroup reduction)
@@ -843,50 +892,6 @@ __device__ __forceinline__ int64_t row_start(const int64_t* lens, int64_t b, int
     int64_t tot = 0;
     for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += part[w];
     return tot;
-}
-
-template <int DT>
-__global__ __launch_bounds__(256) void accept_finalize_kernel(FinArgs a) {
-    __shared__ uint64_t red[4];
-    const int64_t b = blockIdx.x;
-    const int kd = a.k;
-    const int64_t start = row_start(a.lens, b, kd);
-    const int64_t L = a.lens != nullptr ? a.lens[b] : kd + 1;
-    int64_t n = 0;
-    while (n < L - 1 && n < kd && start + n < a.n_pos && a.rec[start + n].acc) ++n;
-    const int64_t pos = min(start + n, a.n_pos - 1);
-    const PosRecord r = a.rec[pos];
-    int64_t winner = r.race;
-    if (r.flags & kFlagDense) {
-        const bool bonus = (n == L - 1);
-        const int64_t qn = n < kd - 1 ? n : kd - 1;
-        const float* qrow = a.q + (b * kd + qn) * a.vocab;
-        const float* erow = a.noise + b * a.vocab;
-        const char* row = static_cast<const char*>(a.logits) + pos * a.row_stride * nvs::dtype_size(DT);
-        const uint32_t theta_key = r.theta == -INFINITY ? 0u : nvs::float_key(r.theta);
-        const float mu = (r.m == -INFINITY) ? 0.f : r.m;
-        const bool unit_temp = (r.temp == 1.f);
-        uint64_t best = 0;
-        for (int64_t i = threadIdx.x; i < a.vocab; i += blockDim.x) {
-            const float s = scale_logit(nvs::load_as_float<DT>(row, i), r.temp, unit_temp);
-            const float p = (sel_key(s) >= theta_key && s == s) ? expf(s - mu) / r.z : 0.f;
-            const float w = bonus ? p : fmaxf(p - qrow[i], 0.f);
-            const float score = w / erow[i];
-            const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
-                                 static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
-            best = best > k64 ? best : k64;
-        }
-        best = wave_max_u64(best);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
-        __syncthreads();
-        uint64_t all = 0;
-        for (int w = 0; w < 4; ++w) all = red[w] > all ? red[w] : all;
-        winner = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(all));
-    }
-    if (threadIdx.x == 0) {
-        a.n_accept[b] = n;
-        a.tail[b] = winner;
-    }
 }
 
 // ---------------------------------------------------------------- dense race kernels
@@ -1283,13 +1288,13 @@ extern "C" int nvs_accept_greedy(const void* logits, int logits_dtype, int64_t l
     return nvs::check_launch("accept_greedy finalize kernel");
 }
 
+// Workspace of the fused accept: one 32-byte record per position (the per-row counters are a separate argument).
 extern "C" int nvs_spec_accept_workspace_size(int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
                                               int max_top_k, size_t* bytes) {
     nvs::clear_error();
-    (void)batch;
     (void)num_drafts;
     (void)vocab;
-    NVS_CHECK(bytes != nullptr && n_pos >= 0, NVS_ERR_INVALID, "spec_accept_workspace_size: bad args");
+    NVS_CHECK(bytes != nullptr && n_pos >= 0 && batch >= 0, NVS_ERR_INVALID, "spec_accept_workspace_size: bad args");
     const int st = check_topk(max_top_k);
     if (st != NVS_OK) return st;
     *bytes = static_cast<size_t>(n_pos) * sizeof(PosRecord);
@@ -1300,8 +1305,8 @@ extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t log
                                const float* temperatures, const int64_t* top_k, const float* top_p, int max_top_k,
                                int has_top_p, const float* q, const int64_t* drafts, const int64_t* verified_lens,
                                const float* uniforms, const float* noise, int64_t batch, int num_drafts,
-                               int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+                               int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail,
+                               int32_t* row_counters, void* workspace, size_t workspace_bytes, void* stream) {
     nvs::clear_error();
     int st = check_dtype(logits_dtype);
     if (st != NVS_OK) return st;
@@ -1310,7 +1315,7 @@ extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t log
     st = common_select_checks(logits, logits_row_stride, n_pos, vocab, 1, max_top_k, top_k);
     if (st != NVS_OK) return st;
     if (batch == 0) return NVS_OK;
-    NVS_CHECK(temperatures && q && uniforms && noise, NVS_ERR_INVALID, "spec_accept: null pointer");
+    NVS_CHECK(temperatures && q && uniforms && noise && row_counters, NVS_ERR_INVALID, "spec_accept: null pointer");
     NVS_CHECK(!has_top_p || top_p != nullptr, NVS_ERR_INVALID, "spec_accept: has_top_p needs top_p");
     NVS_CHECK(verified_lens != nullptr || n_pos == batch * (num_drafts + 1), NVS_ERR_INVALID,
               "spec_accept: logits have %lld positions, expected batch*(k+1) = %lld", (long long)n_pos,
@@ -1337,27 +1342,8 @@ extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t log
     a.batch = batch;
     a.k = num_drafts;
     a.rec = static_cast<PosRecord*>(workspace);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    st = launch_select<kModeAccept>(logits_dtype, a, s);
-    if (st != NVS_OK) return st;
-    FinArgs f{};
-    f.logits = logits;
-    f.row_stride = logits_row_stride;
-    f.vocab = vocab;
-    f.q = q;
-    f.drafts = drafts;
-    f.lens = verified_lens;
-    f.noise = noise;
-    f.batch = batch;
-    f.n_pos = n_pos;
-    f.k = num_drafts;
-    f.rec = a.rec;
-    f.n_accept = n_accept;
-    f.tail = tail;
-    switch (logits_dtype) {
-        case NVS_DTYPE_F32: hipLaunchKernelGGL(accept_finalize_kernel<NVS_DTYPE_F32>, dim3(batch), dim3(256), 0, s, f); break;
-        case NVS_DTYPE_BF16: hipLaunchKernelGGL(accept_finalize_kernel<NVS_DTYPE_BF16>, dim3(batch), dim3(256), 0, s, f); break;
-        default: hipLaunchKernelGGL(accept_finalize_kernel<NVS_DTYPE_F16>, dim3(batch), dim3(256), 0, s, f); break;
-    }
-    return nvs::check_launch("spec_accept finalize kernel");
+    a.counters = row_counters;
+    a.n_accept = n_accept;
+    a.tail = tail;
+    return launch_select<kModeAccept>(logits_dtype, a, static_cast<hipStream_t>(stream));
 }

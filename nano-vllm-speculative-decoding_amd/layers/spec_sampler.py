@@ -268,33 +268,8 @@ def accept_from_logits(target_logits: torch.Tensor, draft_probs: torch.Tensor, d
     assert sampling.temperatures is not None, "greedy batches use accept_greedy(_varlen)"
     _lib.require_device(target_logits, draft_probs, drafts, verified_lens, sampling.temperatures)
     batch_size, num_drafts = drafts.shape
-    rows, n_pos, row_stride = _rows_view(target_logits)
-    vocab = target_logits.shape[-1]
-    uniforms, noise = _draws(batch_size, num_drafts, vocab, target_logits.device, generator)
-    q = _contig(draft_probs, torch.float32)
-    drafts_c = _contig(drafts, torch.int64)
-    lens = _contig(verified_lens, torch.int64)
-    temps = _contig(sampling.temperatures, torch.float32)
-    top_k = _contig(sampling.top_k, torch.int64)
-    top_p = _contig(sampling.top_p, torch.float32)
-    n_accept = torch.empty(batch_size, dtype=torch.int64, device=target_logits.device)
-    tail = torch.empty(batch_size, dtype=torch.int64, device=target_logits.device)
-    if batch_size == 0:
-        return n_accept, tail
-    assert q.shape == (batch_size, num_drafts, vocab), f"draft_probs {tuple(q.shape)} is not [B, k, V]"
-    lib = _lib.load()
-    nbytes = _lib.size_out()
-    _lib.check(lib.nvs_spec_accept_workspace_size(batch_size, num_drafts, n_pos, vocab, sampling.max_top_k,
-                                                  ctypes.byref(nbytes)),
-               "spec_accept_workspace_size")
-    ws = _lib.workspace(nbytes.value, target_logits.device)
-    _lib.check(lib.nvs_spec_accept(rows.data_ptr(), _lib.dtype_code(rows.dtype), row_stride, temps.data_ptr(),
-                                   top_k.data_ptr(), top_p.data_ptr(), sampling.max_top_k, int(sampling.has_top_p),
-                                   q.data_ptr(), drafts_c.data_ptr(), _lib.ptr(lens), uniforms.data_ptr(),
-                                   noise.data_ptr(), batch_size, num_drafts, n_pos, vocab, n_accept.data_ptr(),
-                                   tail.data_ptr(), _lib.ptr(ws), nbytes.value, _lib.stream_of(target_logits)),
-               "spec_accept")
-    return n_accept, tail
+    uniforms, noise = _draws(batch_size, num_drafts, target_logits.shape[-1], target_logits.device, generator)
+    return spec_accept_with_draws(target_logits, draft_probs, drafts, sampling, verified_lens, uniforms, noise)
 
 
 def spec_accept_with_draws(target_logits: torch.Tensor, draft_probs: torch.Tensor, drafts: torch.Tensor,
@@ -302,7 +277,8 @@ def spec_accept_with_draws(target_logits: torch.Tensor, draft_probs: torch.Tenso
                            noise: torch.Tensor, workspace: torch.Tensor | None = None
                            ) -> tuple[torch.Tensor, torch.Tensor]:
     """accept_from_logits with the uniforms [B, k] and noise [B, V] supplied by the caller (tests, benchmarks,
-    a caller that draws them elsewhere). workspace: optional preallocated uint8 buffer."""
+    a caller that draws them elsewhere). workspace: optional uint8 scratch buffer for the per-position records.
+    The per-row counters live in a persistent zero-filled buffer that every call leaves zero."""
     _lib.require_device(target_logits, draft_probs, drafts, verified_lens, uniforms, noise)
     batch_size, num_drafts = drafts.shape
     rows, n_pos, row_stride = _rows_view(target_logits)
@@ -324,13 +300,16 @@ def spec_accept_with_draws(target_logits: torch.Tensor, draft_probs: torch.Tenso
     _lib.check(lib.nvs_spec_accept_workspace_size(batch_size, num_drafts, n_pos, vocab, sampling.max_top_k,
                                                   ctypes.byref(nbytes)),
                "spec_accept_workspace_size")
+    assert q.shape == (batch_size, num_drafts, vocab), f"draft_probs {tuple(q.shape)} is not [B, k, V]"
     if workspace is None or workspace.numel() < nbytes.value:
-        workspace = _lib.workspace(nbytes.value, target_logits.device)
+        workspace = _lib.workspace(max(nbytes.value, 1), target_logits.device)
+    counters = _lib.persistent_workspace("spec_accept_row_counters", 4 * batch_size, target_logits.device)
     _lib.check(lib.nvs_spec_accept(rows.data_ptr(), _lib.dtype_code(rows.dtype), row_stride, temps.data_ptr(),
                                    top_k.data_ptr(), top_p.data_ptr(), sampling.max_top_k, int(sampling.has_top_p),
                                    q.data_ptr(), drafts_c.data_ptr(), _lib.ptr(lens), u.data_ptr(), e.data_ptr(),
                                    batch_size, num_drafts, n_pos, vocab, n_accept.data_ptr(), tail.data_ptr(),
-                                   _lib.ptr(workspace), nbytes.value, _lib.stream_of(target_logits)),
+                                   counters.data_ptr(), workspace.data_ptr(), workspace.numel(),
+                                   _lib.stream_of(target_logits)),
                "spec_accept")
     return n_accept, tail
 

@@ -63,7 +63,7 @@ def attn_args(**over):
     (dict(cu_q=None, cu_k=None, ctx=None), _lib.NVS_ERR_INVALID),
     (dict(scale=0.0), _lib.NVS_ERR_INVALID),
     (dict(bt_width=0), _lib.NVS_ERR_INVALID),
-    (dict(rows=64, mk=4096), _lib.NVS_ERR_WORKSPACE),
+    (dict(rows=1, mk=4096), _lib.NVS_ERR_WORKSPACE),   # one row: the plan splits its keys, partials needed
 ])
 def test_attention_rejects_bad_arguments_without_launching(lib, over, status):
     assert lib.nvs_paged_attention(*attn_args(**over)) == status
@@ -72,11 +72,15 @@ def test_attention_rejects_bad_arguments_without_launching(lib, over, status):
 
 def test_attention_workspace_plan(lib):
     n = ctypes.c_size_t()
+    # batch 64 x 8 kv heads fills one resident round: unsplit, no partials
     assert lib.nvs_paged_attention_workspace_size(64, 32, 8, 128, 8, 4096, ctypes.byref(n)) == 0
+    assert n.value == 0
+    # batch 2: the keys are split to fill the chip, partials need a workspace
+    assert lib.nvs_paged_attention_workspace_size(2, 32, 8, 128, 8, 4096, ctypes.byref(n)) == 0
     assert n.value > 0
     small = ctypes.c_size_t()
     assert lib.nvs_paged_attention_workspace_size(1, 32, 8, 128, 8, 64, ctypes.byref(small)) == 0
-    assert small.value == 0            # one split: no partials
+    assert small.value == 0            # 64 keys: one split, no partials
     assert lib.nvs_paged_attention_workspace_size(1, 32, 8, 64, 8, 64, ctypes.byref(small)) == _lib.NVS_ERR_UNSUPPORTED
 
 
@@ -84,14 +88,14 @@ def test_sampler_rejects_bad_arguments_without_launching(lib):
     n = ctypes.c_size_t()
     assert lib.nvs_spec_accept_workspace_size(64, 7, 512, 151936, 2000, ctypes.byref(n)) == _lib.NVS_ERR_UNSUPPORTED
     assert lib.nvs_spec_accept_workspace_size(64, 7, 512, 151936, 64, ctypes.byref(n)) == 0
-    assert n.value == 512 * 32
+    assert n.value == 512 * 32              # a 32-byte record per position
     # fixed-length call whose position count is not B*(k+1)
     st = lib.nvs_spec_accept(1 << 20, _lib.DTYPE_F32, 100, 1 << 20, 1 << 20, 1 << 20, 64, 0, 1 << 20, 1 << 20, None,
-                             1 << 20, 1 << 20, 4, 7, 31, 100, 1 << 20, 1 << 20, 1 << 20, 1024, None)
+                             1 << 20, 1 << 20, 4, 7, 31, 100, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 1024, None)
     assert st == _lib.NVS_ERR_INVALID
     # workspace too small
     st = lib.nvs_spec_accept(1 << 20, _lib.DTYPE_F32, 100, 1 << 20, 1 << 20, 1 << 20, 64, 0, 1 << 20, 1 << 20, None,
-                             1 << 20, 1 << 20, 4, 7, 32, 100, 1 << 20, 1 << 20, 1 << 20, 16, None)
+                             1 << 20, 1 << 20, 4, 7, 32, 100, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 16, None)
     assert st == _lib.NVS_ERR_WORKSPACE
     assert lib.nvs_probs_from_logits(1 << 20, 9, 100, 4, 100, 1, 1 << 20, None, None, 0, 0, 1 << 20, None, 0,
                                      None) == _lib.NVS_ERR_INVALID

@@ -189,6 +189,37 @@ def test_fused_accept_is_bit_exact(device, name, kwargs):
     print(f"{name}: accepted {n_got.float().mean():.2f} of {case.drafts.shape[1]} on average")
 
 
+def test_fused_accept_repeats_and_replays_in_a_graph(device):
+    """The per-row counters the fused accept keeps in its workspace return to zero after every call: repeated eager
+    calls and HIP-graph replays give the same (bit-exact) answer."""
+    log_case("fused accept repeated calls and graph replays")
+    case = wl.sampler_case(16, 7, 32000, verified_lens=[1, 8, 3, 5, 2, 7, 4, 6] * 2, draft_probs_fn=draft_probs)
+    n_want, tail_want = run_oracle(case)
+    g = case.to(device)
+    st = ns.SamplingTensors(g.temperatures, g.top_k, g.top_p, case.max_top_k, case.has_top_p, True)
+
+    def call():
+        return ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st, g.verified_lens, g.uniforms, g.noise)
+
+    for _ in range(3):
+        n, tail = call()
+        assert torch.equal(n.cpu(), n_want) and torch.equal(tail.cpu(), tail_want)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        n_g, tail_g = call()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(n_g.cpu(), n_want) and torch.equal(tail_g.cpu(), tail_want)
+        n, tail = call()  # eager work between replays
+        assert torch.equal(n.cpu(), n_want)
+
+
 @pytest.mark.parametrize("varlen", [False, True])
 def test_dense_accept_random_is_bit_exact(device, varlen):
     log_case(f"accept_random dense varlen={varlen}")
