@@ -85,6 +85,10 @@ struct SelArgs {
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// Compiler-only memory fence (keeps LDS accesses of one wave in program order for the compiler; the hardware
+// already executes them in order).
+__device__ __forceinline__ void compiler_fence_s() { asm volatile("" ::: "memory"); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -127,6 +131,20 @@ __device__ __forceinline__ int64_t wave_scan_incl_i64(int64_t v) {
     return v;
 }
 
+// Inclusive prefix sum of one integer per lane over the wave through DPP (no LDS round trips): Hillis-Steele
+// shifts by 1, 2, 4 and 8 inside each 16-lane row, then row 0's total into row 1 and row 2's into row 3
+// (row_bcast:15), then rows 0-1's total into rows 2 and 3 (row_bcast:31). Masked rows and lanes shifted in
+// from outside a row add 0.
+__device__ __forceinline__ int wave_scan_incl_dpp(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1 and 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2 and 3
+    return x;
+}
+
 // Descending bitonic sort of one value per lane across the wave; returns this lane's sorted value.
 __device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v) {
     const int l = lane_id();
@@ -145,10 +163,39 @@ __device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v) {
     return v;
 }
 
+// The 64 largest of two descending wave-sorted lists (one value per lane each), sorted descending: the larger
+// of a[i] and b[63 - i] forms a bitonic sequence holding the 64 largest, which a bitonic merge sorts.
+__device__ __forceinline__ uint32_t wave_merge_top(uint32_t a, uint32_t b) {
+    const int l = lane_id();
+    const uint32_t r = static_cast<uint32_t>(__shfl(static_cast<int>(b), 63 - l));
+    uint32_t v = max(a, r);
+#pragma unroll
+    for (int stride = 32; stride > 0; stride >>= 1) {
+        const uint32_t w = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), stride));
+        v = ((l & stride) == 0) ? max(v, w) : min(v, w);
+    }
+    return v;
+}
+
+// The 64 largest keys of a list of n keys, sorted descending across the wave (key 0 past a shorter list).
+__device__ uint32_t wave_top64(const uint32_t* keys, int n) {
+    const int l = lane_id();
+    uint32_t top = wave_sort_desc(l < n ? keys[l] : 0u);
+    for (int c0 = 64; c0 < n; c0 += 64) {
+        const uint32_t k = c0 + l < n ? keys[c0 + l] : 0u;
+        const uint32_t floor_key = static_cast<uint32_t>(__shfl(static_cast<int>(top), 63));
+        if (__ballot(k > floor_key) == 0ull) continue;
+        top = wave_merge_top(top, wave_sort_desc(k));
+    }
+    return top;
+}
+
 struct SelShared {
     uint32_t ckey[kCap];
     int32_t cidx[kCap];
     uint32_t hist[256];
+    uint32_t whist[kSelWaves][256];  // per-wave radix-select histograms of the streaming pass
+    uint32_t tau_key;                // workgroup-wide lower bound of the K-th largest key (only ever raised)
     uint32_t sortbuf[kMaxTopK];
     float fred[kSelWaves];
     uint32_t ured[kSelWaves];
@@ -159,6 +206,10 @@ struct SelShared {
     int found;       // the position belongs to a batch row (fused accept)
     int last;        // this workgroup finishes its batch row (fused accept)
     uint32_t sel_digit, sel_remaining, sel_greater, sel_equal;
+    float fast_m, fast_z, fast_theta;  // row statistics of the wave-0 epilogue
+    uint32_t wmax[kSelWaves];          // largest key of each wave's list
+    uint32_t wlo[kSelWaves];           // each wave's final lower bound of the K-th largest key
+    int bin_count;                     // keys of the threshold's histogram bin
     int64_t loc[4];  // b, j, L, start
     int64_t fin_n;
     PosRecord fin_rec;
@@ -327,33 +378,33 @@ __device__ void locate(const SelArgs& a, int64_t t, SelShared& sh) {
     __syncthreads();
 }
 
+// Elements per 16-byte piece of a logit row.
 template <int DT>
-__device__ __forceinline__ void load_vals(const void* row, int64_t e0, int64_t vocab, bool vec, float (&v)[kVpt]) {
-    // elements e0 + 4*(i*kSelThreads) + ... : each thread handles kVpt values per batch in 16-byte pieces
-    if constexpr (DT == NVS_DTYPE_F32) {
-        const float* p = static_cast<const float*>(row);
+constexpr int piece_elems() { return DT == NVS_DTYPE_F32 ? 4 : 8; }
+
+// One batch of this thread's values: elements e0 + (i * kSelThreads + thread) * W + c, W elements per 16-byte
+// piece. Branch-free, so the compiler can keep several batches of loads in flight (a branch around a load makes
+// it wait for every outstanding load at the join). VEC (16-byte aligned rows, vocab a multiple of W): one
+// streaming 16-byte load per piece from an address clamped into the row; otherwise element loads from clamped
+// indices. Elements past the vocabulary read as NaN, which every filter rejects.
+template <int DT, bool VEC, bool MASK = true>
+__device__ __forceinline__ void load_vals(const void* row, int64_t e0, int64_t vocab, float (&v)[kVpt]) {
+    constexpr int W = piece_elems<DT>();
 #pragma unroll
-        for (int i = 0; i < kVpt / 4; ++i) {
-            const int64_t e = e0 + (static_cast<int64_t>(i) * kSelThreads + threadIdx.x) * 4;
-            if (vec && e + 4 <= vocab) {
-                // streaming loads: each logit is read once per pass
-                const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + e));
+    for (int i = 0; i < kVpt / W; ++i) {
+        const int64_t e = e0 + (static_cast<int64_t>(i) * kSelThreads + threadIdx.x) * W;
+        if constexpr (VEC) {
+            const int64_t ec = min(e, vocab - W);
+            if constexpr (DT == NVS_DTYPE_F32) {
+                const f32x4 x = __builtin_nontemporal_load(
+                    reinterpret_cast<const f32x4*>(static_cast<const float*>(row) + ec));
                 v[4 * i] = x.x;
                 v[4 * i + 1] = x.y;
                 v[4 * i + 2] = x.z;
                 v[4 * i + 3] = x.w;
             } else {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) v[4 * i + c] = (e + c < vocab) ? p[e + c] : NAN;
-            }
-        }
-    } else {
-        const uint16_t* p = static_cast<const uint16_t*>(row);
-#pragma unroll
-        for (int i = 0; i < kVpt / 8; ++i) {
-            const int64_t e = e0 + (static_cast<int64_t>(i) * kSelThreads + threadIdx.x) * 8;
-            if (vec && e + 8 <= vocab) {
-                const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + e));
+                const u32x4 x = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(row) + ec));
                 const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
@@ -365,9 +416,16 @@ __device__ __forceinline__ void load_vals(const void* row, int64_t e0, int64_t v
                         v[8 * i + 2 * c + 1] = nvs::f16_bits_to_float(static_cast<uint16_t>(w[c] >> 16));
                     }
                 }
-            } else {
+            }
+            if constexpr (MASK) {
 #pragma unroll
-                for (int c = 0; c < 8; ++c) v[8 * i + c] = (e + c < vocab) ? nvs::load_as_float<DT>(row, e + c) : NAN;
+                for (int c = 0; c < W; ++c) v[W * i + c] = (e < vocab) ? v[W * i + c] : NAN;
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < W; ++c) {
+                const float x = nvs::load_as_float<DT>(row, min(e + c, vocab - 1));
+                v[W * i + c] = (e + c < vocab) ? x : NAN;
             }
         }
     }
@@ -385,6 +443,78 @@ __device__ __forceinline__ int64_t val_index(int64_t e0, int vi) {
 
 __device__ __forceinline__ float scale_logit(float x, float temp, bool unit_temp) {
     return unit_temp ? x : x / temp;
+}
+
+// The bin of a 256-bin histogram (bins in increasing key order) that holds the rank-th largest (1-based) of the
+// counted keys, and that key's rank within the bin, found by one wave (every lane gets both).
+__device__ __forceinline__ void wave_pick_bin(const uint32_t* hist, uint32_t rank, uint32_t& bin, uint32_t& rem) {
+    const int l = lane_id();
+    uint32_t h[4];
+    uint32_t tot = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h[i] = hist[4 * l + i];
+        tot += h[i];
+    }
+    uint32_t suf = tot;  // inclusive suffix sum over lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t w = static_cast<uint32_t>(__shfl_down(static_cast<int>(suf), o));
+        if (l + o < 64) suf += w;
+    }
+    uint32_t above = suf - tot;
+    int found_bin = -1;
+    uint32_t found_rem = 0;
+#pragma unroll
+    for (int i = 3; i >= 0; --i) {
+        if (found_bin < 0 && above < rank && rank <= above + h[i]) {
+            found_bin = 4 * l + i;
+            found_rem = rank - above;
+        }
+        above += h[i];
+    }
+    const uint64_t who = __ballot(found_bin >= 0);
+    const int src = who ? static_cast<int>(__ffsll(static_cast<long long>(who))) - 1 : 0;
+    bin = static_cast<uint32_t>(__shfl(found_bin, src));
+    rem = static_cast<uint32_t>(__shfl(static_cast<int>(found_rem), src));
+}
+
+// rank-th largest (1-based) key over n_lists lists (list w at keys + w * stride, counts[w] keys), by one wave
+// alone with its own 256-bin histogram: four 8-bit radix passes, no workgroup barrier. LDS executes one wave's
+// accesses in order; the fences keep the compiler from reordering them. rank must not exceed the total count.
+__device__ uint32_t wave_radix_select_lists(const uint32_t* keys, int stride, const int* counts, int n_lists,
+                                            int rank, uint32_t* hist) {
+    const int l = lane_id();
+    uint32_t prefix = 0u, mask = 0u;
+    uint32_t remaining = static_cast<uint32_t>(rank);
+#pragma unroll 1
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hist[4 * l + i] = 0u;
+        compiler_fence_s();
+        for (int w = 0; w < n_lists; ++w) {
+            const uint32_t* list = keys + w * stride;
+            const int n = counts[w];
+            for (int i = l; i < n; i += 64) {
+                const uint32_t key = list[i];
+                if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+            }
+        }
+        compiler_fence_s();
+        uint32_t digit;
+        wave_pick_bin(hist, remaining, digit, remaining);
+        prefix |= digit << shift;
+        mask |= 255u << shift;
+        compiler_fence_s();
+    }
+    return prefix;
+}
+
+// rank-th largest (1-based) of the n keys at list[0..n), by one wave (see wave_radix_select_lists).
+__device__ uint32_t wave_radix_select(const uint32_t* list, int n, int rank, uint32_t* hist) {
+    const int counts[1] = {n};
+    return wave_radix_select_lists(list, 0, counts, 1, rank, hist);
 }
 
 // Key of a value for selection; NaN padding (past the vocabulary) maps to 0, below every real value.
@@ -477,13 +607,13 @@ struct RowStats {
 };
 
 // Full-row exact path (candidate list overflowed): radix select on the row, then rebuild the candidate list.
-template <int DT>
-__device__ RowStats exact_row_stats(const SelArgs& a, const void* row, bool vec, float temp, bool unit_temp,
+template <int DT, bool VEC>
+__device__ RowStats exact_row_stats(const SelArgs& a, const void* row, float temp, bool unit_temp,
                                     int rank, int K, float top_p, SelShared& sh) {
     auto for_each = [&](auto&& fn) {
         for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
             float v[kVpt];
-            load_vals<DT>(row, e0, a.vocab, vec, v);
+            load_vals<DT, VEC>(row, e0, a.vocab, v);
 #pragma unroll
             for (int vi = 0; vi < kVpt; ++vi) {
                 const uint32_t key = sel_key(scale_logit(v[vi], temp, unit_temp));
@@ -504,7 +634,7 @@ __device__ RowStats exact_row_stats(const SelArgs& a, const void* row, bool vec,
     const uint32_t floor_key = fits ? thr_key : thr_key + 1u;
     for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
         float v[kVpt];
-        load_vals<DT>(row, e0, a.vocab, vec, v);
+        load_vals<DT, VEC>(row, e0, a.vocab, v);
         uint32_t keys[kVpt];
 #pragma unroll
         for (int vi = 0; vi < kVpt; ++vi) keys[vi] = sel_key(scale_logit(v[vi], temp, unit_temp));
@@ -546,7 +676,7 @@ __device__ RowStats exact_row_stats(const SelArgs& a, const void* row, bool vec,
     } else {
         for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
             float v[kVpt];
-            load_vals<DT>(row, e0, a.vocab, vec, v);
+            load_vals<DT, VEC>(row, e0, a.vocab, v);
 #pragma unroll
             for (int vi = 0; vi < kVpt; ++vi) {
                 const float s = scale_logit(v[vi], temp, unit_temp);
@@ -560,21 +690,39 @@ __device__ RowStats exact_row_stats(const SelArgs& a, const void* row, bool vec,
 
 // Finish batch row b of the fused accept (run by the workgroup whose position arrived last): the accepted prefix
 // n from the positions' decisions, then the tail = the race of position start + n, which that position already ran
-// over its kept set, or, for a row that does not truncate, a race over the whole vocabulary run here.
+// over its kept set, or, for a row that does not truncate, a race over the whole vocabulary run here. The caller
+// has acquired the other positions' records (count_position).
 template <int DT>
 __device__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L, SelShared& sh) {
     const int kd = a.k;
-    if (threadIdx.x == 0) {
-        __threadfence();  // acquire: the other positions' records
-        int64_t n = 0;
-        while (n < L - 1 && n < kd && start + n < a.n_pos && a.rec[start + n].acc) ++n;
-        sh.fin_n = n;
-        sh.fin_rec = a.rec[min(start + n, a.n_pos - 1)];
+    if (threadIdx.x < 64) {
+        // wave 0: lane i loads the record of position start + c0 + i, all in one round trip; the first position
+        // that is rejected or cannot be accepted ends the prefix and its record gives the tail
+        const int lane = threadIdx.x;
+        const int64_t lim = min(min(L - 1, static_cast<int64_t>(kd)), a.n_pos - start);   // n stays <= lim
+        for (int64_t c0 = 0;; c0 += 64) {
+            const int64_t pos = min(start + c0 + lane, a.n_pos - 1);
+            const PosRecord r = a.rec[pos];
+            const bool stop = (c0 + lane >= lim) || !r.acc;
+            const uint64_t bal = __ballot(stop);
+            if (bal == 0ull) continue;   // all 64 accepted: the next 64
+            const int first = __ffsll(static_cast<long long>(bal)) - 1;
+            if (lane == first) {
+                const int64_t n = c0 + first;
+                sh.fin_n = n;
+                sh.fin_rec = r;
+                if (!(r.flags & kFlagDense)) {   // the tail is that position's own race: the row is done
+                    a.n_accept[b] = n;
+                    a.tail[b] = r.race;
+                    a.counters[b] = 0;   // ready for the next call
+                }
+            }
+            break;
+        }
     }
     __syncthreads();
     const int64_t n = sh.fin_n;
     const PosRecord r = sh.fin_rec;
-    int64_t winner = r.race;
     if (r.flags & kFlagDense) {
         const int64_t pos = min(start + n, a.n_pos - 1);
         const bool bonus = (n == L - 1);
@@ -596,17 +744,28 @@ __device__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L
             best = best > k64 ? best : k64;
         }
         best = block_max_u64(best, sh);
-        winner = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
-    }
-    if (threadIdx.x == 0) {
-        a.n_accept[b] = n;
-        a.tail[b] = winner;
-        a.counters[b] = 0;  // ready for the next call
+        if (threadIdx.x == 0) {
+            a.n_accept[b] = n;
+            a.tail[b] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
+            a.counters[b] = 0;  // ready for the next call
+        }
     }
 }
 
-template <int DT, int MODE>
-__global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
+// Count a finished position of batch row b: a release add on the row's counter, so the position's record
+// (stored before) is visible to whichever position counts last; that one acquires every record of the row and
+// finishes it. Returns whether this position counted last.
+__device__ __forceinline__ bool count_position(int* counter, int64_t n_positions) {
+    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = before == static_cast<int>(n_positions) - 1;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return last;
+}
+
+template <int DT, int MODE, bool VEC>
+// At most 128 VGPRs (4 waves per SIMD): two 8-wave workgroups per CU, so the 512 positions of a verify batch
+// run in one round on 256 CUs.
+__global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
     __shared__ SelShared sh;
     const int64_t t = blockIdx.x;
     if (threadIdx.x == 0) {
@@ -614,6 +773,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
         sh.overflow = 0;
         sh.found = 0;
         sh.last = 0;
+        sh.tau_key = 0u;
         sh.loc[0] = sh.loc[1] = sh.loc[3] = 0;
         sh.loc[2] = 1;
     }
@@ -633,17 +793,40 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
     const bool truncating = K > 0 && tk > 0;
     const int rank = truncating ? static_cast<int>(min(tk, static_cast<int64_t>(K))) : 0;
     const char* row = static_cast<const char*>(a.logits) + t * a.row_stride * nvs::dtype_size(DT);
-    const bool vec = nvs::aligned16(a.logits) && ((a.row_stride * nvs::dtype_size(DT)) % 16 == 0);
+
+    // Fused accept: the accept test's inputs (draft token d, the logit at d, q at d, the uniform) do not depend on
+    // the pass over the row, so every thread requests them (same addresses, clamped into range: no branch) before
+    // the row streams, and they arrive while it does. dec_valid: this position verifies a draft inside the
+    // vocabulary (an out-of-vocabulary draft is never accepted).
+    bool dec_valid = false;
+    float dec_x = 0.f, dec_q = 0.f, dec_u = 0.f;
+    int64_t dec_slot = 0, dec_d = 0;
+    if constexpr (MODE == kModeAccept) {
+        const int64_t b = sh.loc[0], j = sh.loc[1], L = sh.loc[2];
+        dec_slot = b * a.k + min(j, static_cast<int64_t>(a.k) - 1);
+        dec_d = a.drafts[dec_slot];
+        dec_valid = (j < L - 1) && (j < a.k) && (dec_d >= 0) && (dec_d < a.vocab);
+    }
+    auto load_decision = [&]() {
+        if constexpr (MODE == kModeAccept) {
+            const int64_t dc = min(max(dec_d, int64_t{0}), a.vocab - 1);
+            dec_x = nvs::load_as_float<DT>(row, dc);
+            dec_q = a.q[dec_slot * a.vocab + dc];
+            dec_u = a.uniforms[dec_slot];
+        }
+    };
 
     RowStats rs;
     rs.dense = !truncating;
     rs.theta = -INFINITY;
+    bool record_done = false;   // the wave-0 epilogue already wrote this position's record
     if (!truncating) {
+        load_decision();
         // online max / sum-exp over the whole row
         float m = -INFINITY, z = 0.f;
         for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
             float v[kVpt];
-            load_vals<DT>(row, e0, a.vocab, vec, v);
+            load_vals<DT, VEC>(row, e0, a.vocab, v);
 #pragma unroll
             for (int vi = 0; vi < kVpt; ++vi) {
                 const float s = scale_logit(v[vi], temp, unit_temp);
@@ -664,25 +847,72 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
         rs.m = mall;
     } else {
         // ---- one pass: every element >= tau, a lower bound of the K-th largest, joins its wave's candidate list.
-        // tau comes from the first batch: each wave's ceil(K/8)-th largest lane maximum, the smallest over the 8
+        // tau starts from the first batch: each wave's ceil(K/8)-th largest lane maximum, the smallest over the 8
         // waves, so at least K elements lie at or above it. After that the pass has no workgroup barrier: a wave
-        // appends to its own list, and a list that overflows sends the row to the exact path.
+        // appends to its own list; when the list passes half its capacity the wave takes the exact K-th largest
+        // of its own list (a lower bound of the row's too), raises tau to it, drops what lies below and publishes
+        // the bound to the other waves through one LDS word they read each batch. A wave whose list still
+        // overflows sends the row to the exact path.
         const int wave = threadIdx.x >> 6;
+        const int lane = lane_id();
         uint32_t* wkey = sh.ckey + wave * kWaveCap;
         int32_t* widx = sh.cidx + wave * kWaveCap;
-        const uint64_t below = (lane_id() == 0) ? 0ull : (~0ull >> (64 - lane_id()));
+        const int nb = static_cast<int>((a.vocab + kBatch - 1) / kBatch);
+        uint32_t tau_key = 0xffffffffu;
         float tau = INFINITY;
         int wcount = 0;
-        float vcur[kVpt];
-        load_vals<DT>(row, 0, a.vocab, vec, vcur);
-        for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
-            float vnext[kVpt];
-            const bool more = e0 + kBatch < a.vocab;
-            if (more) load_vals<DT>(row, e0 + kBatch, a.vocab, vec, vnext);
-            float sv[kVpt];
+        uint32_t hmax = 0u;   // largest key this lane appended
+        bool overflow = false;
+
+        // The K-th largest of this wave's list becomes its bound; entries below it leave the list.
+        auto refine = [&]() {
+            const uint32_t kth = K <= 64 ? static_cast<uint32_t>(__shfl(static_cast<int>(wave_top64(wkey, wcount)), K - 1))
+                                         : wave_radix_select(wkey, wcount, K, sh.whist[wave]);
+            if (kth > tau_key || tau_key == 0xffffffffu) {
+                tau_key = kth;
+                tau = nvs::key_float(kth);
+                atomicMax(&sh.tau_key, kth);
+            }
+            constexpr int kPer = kWaveCap / 64;
+            uint32_t kk[kPer];
+            int32_t ii[kPer];
 #pragma unroll
-            for (int vi = 0; vi < kVpt; ++vi) sv[vi] = scale_logit(vcur[vi], temp, unit_temp);
-            if (e0 == 0) {
+            for (int j = 0; j < kPer; ++j) {
+                const int c = lane + 64 * j;
+                kk[j] = c < wcount ? wkey[c] : 0u;
+                ii[j] = c < wcount ? widx[c] : 0;
+            }
+            compiler_fence_s();
+            const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+            int kept = 0;
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                const bool keep = kk[j] != 0u && kk[j] >= tau_key;
+                const uint64_t bal = __ballot(keep);
+                if (keep) {
+                    const int pos = kept + __popcll(bal & below);
+                    wkey[pos] = kk[j];
+                    widx[pos] = ii[j];
+                }
+                kept += __popcll(bal);
+            }
+            compiler_fence_s();
+            wcount = kept;
+        };
+
+        // Filter one batch. Most batches hold no element at or above tau in the whole wave: one max, one compare,
+        // one ballot. Otherwise the passing values are appended to the wave's list.
+        auto filter = [&](float (&sv)[kVpt], int bi) {   // scales the buffer in place (it is reloaded next)
+            const int64_t e0 = static_cast<int64_t>(bi) * kBatch;
+            if (!unit_temp) {
+#pragma unroll
+                for (int vi = 0; vi < kVpt; ++vi) sv[vi] = sv[vi] / temp;
+            }
+            if (e0 + kBatch > a.vocab) {   // the last, partial batch: elements past the row are NaN
+#pragma unroll
+                for (int vi = 0; vi < kVpt; ++vi) sv[vi] = val_index<DT>(e0, vi) < a.vocab ? sv[vi] : NAN;
+            }
+            if (bi == 0) {
                 uint32_t tmax = 0u;
 #pragma unroll
                 for (int vi = 0; vi < kVpt; ++vi) tmax = max(tmax, sel_key(sv[vi]));
@@ -692,42 +922,239 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
                     const uint32_t sorted = wave_sort_desc(tmax);
                     bound = static_cast<uint32_t>(__shfl(static_cast<int>(sorted), rw - 1));
                 }
-                if (lane_id() == 0) sh.ured[wave] = bound;
+                if (lane == 0) sh.ured[wave] = bound;
                 __syncthreads();
                 uint32_t b = 0xffffffffu;
                 for (int w = 0; w < kSelWaves; ++w) b = min(b, sh.ured[w]);
+                tau_key = b;
                 tau = (b == 0u) ? -INFINITY : nvs::key_float(b);   // NaN never passes a >= test
             }
-            bool any = false;
+            const uint32_t shared_key = __hip_atomic_load(&sh.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            // every path reads the whole buffer first, so its loads are complete before the buffer is reloaded
+            float hi = sv[0];
 #pragma unroll
-            for (int vi = 0; vi < kVpt; ++vi) any |= (sv[vi] >= tau);
-            if (__ballot(any) != 0ull) {
+            for (int vi = 1; vi < kVpt; ++vi) hi = fmaxf(hi, sv[vi]);
+            if (overflow || __ballot(hi >= tau) == 0ull) return;
+            if (shared_key > tau_key) {   // another wave raised the bound
+                tau_key = shared_key;
+                tau = nvs::key_float(shared_key);
+            }
+            // each lane marks its passing values in a bitmask and writes them after its wave prefix of the counts
+            uint32_t pass = 0u;
 #pragma unroll
-                for (int vi = 0; vi < kVpt; ++vi) {
-                    const bool pass = sv[vi] >= tau;
-                    const uint64_t bal = __ballot(pass);
-                    if (pass) {
-                        const int pos = wcount + __popcll(bal & below);
-                        if (pos < kWaveCap) {
-                            wkey[pos] = nvs::float_key(sv[vi]);
-                            widx[pos] = static_cast<int32_t>(val_index<DT>(e0, vi));
-                        }
-                    }
-                    wcount += __popcll(bal);
+            for (int vi = 0; vi < kVpt; ++vi) pass |= (sv[vi] >= tau ? 1u : 0u) << vi;
+            const int c = __popc(pass);
+            const int incl = wave_scan_incl_dpp(c);
+            const int total = __builtin_amdgcn_readlane(incl, 63);
+            if (wcount + total > kWaveCap) {
+                overflow = true;   // the exact path re-reads the row
+                return;
+            }
+            int pos = wcount + incl - c;
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) {
+                if ((pass >> vi) & 1u) {
+                    const uint32_t key = nvs::float_key(sv[vi]);
+                    wkey[pos] = key;
+                    widx[pos] = static_cast<int32_t>(val_index<DT>(e0, vi));
+                    hmax = max(hmax, key);
+                    ++pos;
                 }
-                if (wcount > kWaveCap) break;   // overflow: the exact path re-reads the row
             }
-            if (more) {
-#pragma unroll
-                for (int vi = 0; vi < kVpt; ++vi) vcur[vi] = vnext[vi];
-            }
+            wcount += total;
+            if (wcount > kWaveCap / 2 && wcount >= K) refine();
+        };
+
+        // Three register buffers in a ring, unrolled so no values are copied: while one batch is filtered the
+        // next two are in flight.
+        float ra[kVpt], rb[kVpt], rc[kVpt];
+        load_vals<DT, VEC, false>(row, 0, a.vocab, ra);
+        if (nb > 1) load_vals<DT, VEC, false>(row, kBatch, a.vocab, rb);
+        load_decision();   // after the draft token, behind the first two batches
+        for (int bi = 0;;) {
+            if (bi + 2 < nb) load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rc);
+            filter(ra, bi);
+            if (++bi >= nb) break;
+            if (bi + 2 < nb) load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, ra);
+            filter(rb, bi);
+            if (++bi >= nb) break;
+            if (bi + 2 < nb) load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rb);
+            filter(rc, bi);
+            if (++bi >= nb) break;
         }
-        if (lane_id() == 0) {
+        if (overflow) wcount = kWaveCap + 1;
+        const uint32_t wave_hi = wave_max_u32(hmax);
+        if (lane == 0) {
             sh.wcount[wave] = min(wcount, kWaveCap);
             if (wcount > kWaveCap) sh.overflow = 1;
+            sh.wlo[wave] = tau_key;
+            sh.wmax[wave] = wave_hi;
+        }
+        if (threadIdx.x < 256) sh.hist[threadIdx.x] = 0u;
+        if (threadIdx.x == 0) {
+            sh.count = 0;
+            sh.bin_count = 0;
         }
         __syncthreads();
-        if (!sh.overflow) {
+        int listed = 0;
+        for (int w = 0; w < kSelWaves; ++w) listed += sh.wcount[w];
+        // fewer listed keys than the rank (NaN logits never join a list): the exact path decides the row
+        bool exact = sh.overflow || listed < rank;
+
+        // Without top-p: every key at or above lo (the largest of the waves' bounds, still at most the K-th
+        // largest, and every such key is listed) goes into one 256-bin histogram over [lo, hi], the bins spread
+        // over that range so few keys share one. The bin holding the rank-th largest and the bins above it hold
+        // few keys; they move to one short list (the bin's own keys also to a second), where wave 0 finds the
+        // threshold by counting and finishes the row.
+        constexpr int kTopCap = kSelWaves * 64;   // short-list capacity: indices follow the keys in sortbuf
+        uint32_t* bin_keys = &sh.whist[0][0];
+        bool fast = !exact && !a.has_top_p;
+        uint32_t lo = 0u, hi = 0u, bin = 0u, bin_rank = 0u;
+        int shift = 0;
+        if (fast) {
+            for (int w = 0; w < kSelWaves; ++w) {
+                lo = max(lo, sh.wlo[w]);
+                hi = max(hi, sh.wmax[w]);
+            }
+            const uint32_t range = hi - lo;
+            shift = range < 256u ? 0 : 24 - __clz(range);
+            const int cnt = sh.wcount[wave];
+            for (int i = lane; i < cnt; i += 64) {
+                const uint32_t key = wkey[i];
+                if (key >= lo) atomicAdd(&sh.hist[(key - lo) >> shift], 1u);
+            }
+            __syncthreads();
+            wave_pick_bin(sh.hist, static_cast<uint32_t>(rank), bin, bin_rank);
+            // the same on every wave; a histogram with fewer than rank keys (never expected) goes to the exact path
+            const bool picked = bin < 256u;
+            const int n_top = picked ? rank - static_cast<int>(bin_rank) + static_cast<int>(sh.hist[bin]) : 0;
+            exact = !picked;
+            fast = picked && n_top <= kTopCap;
+            if (fast) {
+                const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+                for (int c0 = 0; c0 < cnt; c0 += 64) {
+                    const int i = c0 + lane;
+                    const uint32_t key = i < cnt ? wkey[i] : 0u;
+                    const bool in = i < cnt && key >= lo;
+                    const uint32_t d = (key - lo) >> shift;
+                    const bool take = in && d >= bin;
+                    const uint64_t bal = __ballot(take);
+                    if (bal == 0ull) continue;
+                    int base = 0;
+                    if (lane == 0) base = atomicAdd(&sh.count, __popcll(bal));
+                    base = __shfl(base, 0);
+                    const bool at_bin = take && d == bin;
+                    const uint64_t bbal = __ballot(at_bin);
+                    int bbase = 0;
+                    if (lane == 0 && bbal != 0ull) bbase = atomicAdd(&sh.bin_count, __popcll(bbal));
+                    bbase = __shfl(bbase, 0);
+                    if (take) {
+                        const int p = base + __popcll(bal & below);
+                        sh.sortbuf[p] = key;
+                        sh.sortbuf[kTopCap + p] = static_cast<uint32_t>(widx[i]);
+                    }
+                    if (at_bin) bin_keys[bbase + __popcll(bbal & below)] = key;
+                }
+            }
+            __syncthreads();
+        }
+        if (fast) {
+            // Wave 0 finishes the row alone: the threshold, the softmax sum over the kept keys and, for the fused
+            // accept, this position's accept test, its race and its record.
+            if (wave == 0) {
+                // threshold: the largest key of the bin with at least bin_rank keys of the bin at or above it
+                const int nb_keys = sh.bin_count;
+                uint32_t cand = 0u;
+                for (int i = lane; i < nb_keys; i += 64) {
+                    const uint32_t ki_key = bin_keys[i];
+                    uint32_t ge = 0;
+                    for (int jj = 0; jj < nb_keys; ++jj) ge += (bin_keys[jj] >= ki_key) ? 1u : 0u;
+                    if (ge >= bin_rank) cand = max(cand, ki_key);
+                }
+                const uint32_t thr_key = wave_max_u32(cand);
+                const float m = nvs::key_float(hi);
+                const float mu_f = (m == -INFINITY) ? 0.f : m;
+                const int n_top = sh.count;
+                uint32_t kk[kSelWaves];
+                int32_t ki[kSelWaves];
+                float z = 0.f;
+#pragma unroll
+                for (int w = 0; w < kSelWaves; ++w) {
+                    const int c = w * 64 + lane;
+                    kk[w] = c < n_top ? sh.sortbuf[c] : 0u;
+                    ki[w] = c < n_top ? static_cast<int32_t>(sh.sortbuf[kTopCap + c]) : 0;
+                    if (kk[w] >= thr_key) z += expf(nvs::key_float(kk[w]) - mu_f);
+                }
+                z = wave_sum(z);
+                if (lane == 0) {
+                    sh.fast_m = m;
+                    sh.fast_z = z;
+                    sh.fast_theta = nvs::key_float(thr_key);
+                }
+                if constexpr (MODE == kModeAccept) {
+                    const int64_t b = sh.loc[0], j = sh.loc[1], L = sh.loc[2];
+                    const int kd = a.k;
+                    const bool bonus = (j >= L - 1) || (j >= kd);
+                    int acc = 0;
+                    if (lane == 0 && dec_valid) {
+                        const float sd = scale_logit(dec_x, temp, unit_temp);
+                        const float pd = (sel_key(sd) >= thr_key && sel_key(sd) != 0u) ? expf(sd - mu_f) / z : 0.f;
+                        acc = (dec_u * dec_q < pd) ? 1 : 0;
+                    }
+                    const float* qrow = a.q + (b * kd + (bonus ? 0 : j)) * a.vocab;
+                    const float* erow = a.noise + b * a.vocab;
+                    // every load first (index 0 stands in for a pair that is not kept), then the scores
+                    float qv[kSelWaves], ev[kSelWaves];
+#pragma unroll
+                    for (int w = 0; w < kSelWaves; ++w) {
+                        const int64_t ix = kk[w] >= thr_key ? static_cast<int64_t>(ki[w]) : int64_t{0};
+                        qv[w] = bonus ? 0.f : qrow[ix];
+                        ev[w] = erow[ix];
+                    }
+                    uint64_t best = 0;
+#pragma unroll
+                    for (int w = 0; w < kSelWaves; ++w) {
+                        if (kk[w] < thr_key) continue;
+                        const float p = expf(nvs::key_float(kk[w]) - mu_f) / z;
+                        const float wgt = bonus ? p : fmaxf(p - qv[w], 0.f);
+                        const float score = wgt / ev[w];
+                        const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+                                             static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(ki[w]));
+                        best = best > k64 ? best : k64;
+                    }
+                    best = wave_max_u64(best);
+                    if (lane == 0) {
+                        PosRecord r;
+                        r.m = m;
+                        r.z = z;
+                        r.theta = nvs::key_float(thr_key);
+                        r.temp = temp;
+                        r.flags = 0;
+                        r.acc = acc;
+                        int64_t winner = 0;
+                        if (best != 0) {
+                            const float score = nvs::key_float(static_cast<uint32_t>(best >> 32));
+                            // all weights zero: torch's argmax over the zero vector is index 0
+                            winner = (score > 0.f) ? static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best))
+                                                   : int64_t{0};
+                        }
+                        r.race = winner;
+                        a.rec[t] = r;
+                        if (sh.found) {
+                            const int64_t L_eff = min(max(L, int64_t{1}), static_cast<int64_t>(kd) + 1);
+                            sh.last = count_position(&a.counters[b], L_eff) ? 1 : 0;
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            rs.m = sh.fast_m;
+            rs.z = sh.fast_z;
+            rs.theta = sh.fast_theta;
+            rs.dense = false;
+            record_done = true;
+        } else {
+        if (!exact) {
             // the per-wave lists, one after another
             int off = 0, total = 0;
             for (int w = 0; w < kSelWaves; ++w) {
@@ -756,8 +1183,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
             if (threadIdx.x == 0) sh.count = total;
         }
         __syncthreads();
-        if (sh.overflow) {
-            rs = exact_row_stats<DT>(a, row, vec, temp, unit_temp, rank, K, top_p, sh);
+        if (exact) {
+            rs = exact_row_stats<DT, VEC>(a, row, temp, unit_temp, rank, K, top_p, sh);
         } else {
             const int n = sh.count;
             auto each = [&](auto&& fn) {
@@ -791,6 +1218,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
             rs.z = block_sum(z, sh);
             rs.dense = false;
         }
+        }
     }
 
     const uint32_t theta_key = rs.theta == -INFINITY ? 0u : nvs::float_key(rs.theta);
@@ -800,7 +1228,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
         float* orow = a.out + t * a.out_stride;
         for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
             float v[kVpt];
-            load_vals<DT>(row, e0, a.vocab, vec, v);
+            load_vals<DT, VEC>(row, e0, a.vocab, v);
 #pragma unroll
             for (int vi = 0; vi < kVpt; ++vi) {
                 const int64_t e = val_index<DT>(e0, vi);
@@ -818,17 +1246,18 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
     } else {
         // ---- fused accept: this position's accept test and race
         const int64_t b = sh.loc[0], j = sh.loc[1], L = sh.loc[2];
+        if (record_done) {
+            if (!sh.last) return;
+            finish_row<DT>(a, b, sh.loc[3], L, sh);
+            return;
+        }
         const int kd = a.k;
         const bool bonus = (j >= L - 1) || (j >= kd);
         int acc = 0;
-        if (threadIdx.x == 0 && j < L - 1 && j < kd) {
-            const int64_t d = a.drafts[b * kd + j];
-            if (d >= 0 && d < a.vocab) {  // an out-of-vocabulary draft is never accepted
-                const float sd = scale_logit(nvs::load_as_float<DT>(row, d), temp, unit_temp);
-                const float pd = (sel_key(sd) >= theta_key && sel_key(sd) != 0u) ? expf(sd - mu) / rs.z : 0.f;
-                const float qd = a.q[(b * kd + j) * a.vocab + d];
-                acc = (a.uniforms[b * kd + j] * qd < pd) ? 1 : 0;
-            }
+        if (threadIdx.x == 0 && dec_valid) {
+            const float sd = scale_logit(dec_x, temp, unit_temp);
+            const float pd = (sel_key(sd) >= theta_key && sel_key(sd) != 0u) ? expf(sd - mu) / rs.z : 0.f;
+            acc = (dec_u * dec_q < pd) ? 1 : 0;
         }
         uint64_t best = 0;
         if (!rs.dense) {
@@ -865,11 +1294,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelArgs a) {
             }
             r.race = winner;
             a.rec[t] = r;
-            // release this record, then count the position; the row's last position to arrive finishes the row
-            __threadfence();
+            // count the position; the row's last position to arrive finishes the row
             if (sh.found) {
                 const int64_t L_eff = min(max(L, int64_t{1}), static_cast<int64_t>(kd) + 1);
-                sh.last = (atomicAdd(&a.counters[b], 1) == static_cast<int>(L_eff) - 1);
+                sh.last = count_position(&a.counters[b], L_eff) ? 1 : 0;
             }
         }
         __syncthreads();
@@ -990,17 +1418,16 @@ __global__ __launch_bounds__(64) void race_merge_kernel(RaceArgs a) {
 
 // ---------------------------------------------------------------- greedy
 
-template <int DT>
+template <int DT, bool VEC>
 __global__ __launch_bounds__(kSelThreads) void argmax_kernel(const void* logits, int64_t row_stride, int64_t vocab,
                                                              int64_t* tokens) {
     __shared__ uint64_t red[kSelWaves];
     const int64_t t = blockIdx.x;
     const char* row = static_cast<const char*>(logits) + t * row_stride * nvs::dtype_size(DT);
-    const bool vec = nvs::aligned16(logits) && ((row_stride * nvs::dtype_size(DT)) % 16 == 0);
     uint64_t best = 0;
     for (int64_t e0 = 0; e0 < vocab; e0 += kBatch) {
         float v[kVpt];
-        load_vals<DT>(row, e0, vocab, vec, v);
+        load_vals<DT, VEC>(row, e0, vocab, v);
 #pragma unroll
         for (int vi = 0; vi < kVpt; ++vi) {
             const int64_t e = val_index<DT>(e0, vi);
@@ -1051,15 +1478,45 @@ int check_topk(int max_top_k) {
     return NVS_OK;
 }
 
+// Rows qualify for the 16-byte streaming loads when every row starts 16-byte aligned and the vocabulary is a
+// whole number of 16-byte pieces.
+bool vector_rows(const void* base, int64_t row_stride, int64_t vocab, int dt) {
+    const int es = nvs::dtype_size(dt);
+    const int w = 16 / es;
+    return nvs::aligned16(base) && (row_stride * es) % 16 == 0 && vocab % w == 0;
+}
+
+template <int DT, int MODE>
+void launch_select_dt(const SelArgs& a, bool vec, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(a.n_pos));
+    if (vec) {
+        hipLaunchKernelGGL((select_kernel<DT, MODE, true>), grid, dim3(kSelThreads), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((select_kernel<DT, MODE, false>), grid, dim3(kSelThreads), 0, s, a);
+    }
+}
+
 template <int MODE>
 int launch_select(int dt, const SelArgs& a, hipStream_t s) {
-    const dim3 grid(static_cast<unsigned>(a.n_pos));
+    const bool vec = vector_rows(a.logits, a.row_stride, a.vocab, dt);
     switch (dt) {
-        case NVS_DTYPE_F32: hipLaunchKernelGGL((select_kernel<NVS_DTYPE_F32, MODE>), grid, dim3(kSelThreads), 0, s, a); break;
-        case NVS_DTYPE_BF16: hipLaunchKernelGGL((select_kernel<NVS_DTYPE_BF16, MODE>), grid, dim3(kSelThreads), 0, s, a); break;
-        default: hipLaunchKernelGGL((select_kernel<NVS_DTYPE_F16, MODE>), grid, dim3(kSelThreads), 0, s, a); break;
+        case NVS_DTYPE_F32: launch_select_dt<NVS_DTYPE_F32, MODE>(a, vec, s); break;
+        case NVS_DTYPE_BF16: launch_select_dt<NVS_DTYPE_BF16, MODE>(a, vec, s); break;
+        default: launch_select_dt<NVS_DTYPE_F16, MODE>(a, vec, s); break;
     }
     return nvs::check_launch("sampler select kernel");
+}
+
+template <int DT>
+void launch_argmax(const void* logits, int64_t row_stride, int64_t n_pos, int64_t vocab, int64_t* tokens,
+                   hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(n_pos));
+    if (vector_rows(logits, row_stride, vocab, DT)) {
+        hipLaunchKernelGGL((argmax_kernel<DT, true>), grid, dim3(kSelThreads), 0, s, logits, row_stride, vocab, tokens);
+    } else {
+        hipLaunchKernelGGL((argmax_kernel<DT, false>), grid, dim3(kSelThreads), 0, s, logits, row_stride, vocab,
+                           tokens);
+    }
 }
 
 int64_t race_chunks(int64_t vocab) { return (vocab + kRaceChunk - 1) / kRaceChunk; }
@@ -1275,11 +1732,10 @@ extern "C" int nvs_accept_greedy(const void* logits, int logits_dtype, int64_t l
               "accept_greedy: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
     int64_t* tokens = static_cast<int64_t*>(workspace);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(static_cast<unsigned>(n_pos));
     switch (logits_dtype) {
-        case NVS_DTYPE_F32: hipLaunchKernelGGL(argmax_kernel<NVS_DTYPE_F32>, grid, dim3(kSelThreads), 0, s, logits, logits_row_stride, vocab, tokens); break;
-        case NVS_DTYPE_BF16: hipLaunchKernelGGL(argmax_kernel<NVS_DTYPE_BF16>, grid, dim3(kSelThreads), 0, s, logits, logits_row_stride, vocab, tokens); break;
-        default: hipLaunchKernelGGL(argmax_kernel<NVS_DTYPE_F16>, grid, dim3(kSelThreads), 0, s, logits, logits_row_stride, vocab, tokens); break;
+        case NVS_DTYPE_F32: launch_argmax<NVS_DTYPE_F32>(logits, logits_row_stride, n_pos, vocab, tokens, s); break;
+        case NVS_DTYPE_BF16: launch_argmax<NVS_DTYPE_BF16>(logits, logits_row_stride, n_pos, vocab, tokens, s); break;
+        default: launch_argmax<NVS_DTYPE_F16>(logits, logits_row_stride, n_pos, vocab, tokens, s); break;
     }
     st = nvs::check_launch("accept_greedy argmax kernel");
     if (st != NVS_OK) return st;
