@@ -30,8 +30,9 @@ constexpr int kSelThreads = 512;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kVpt = 16;                       // values per thread per batch
 constexpr int kBatch = kSelThreads * kVpt;     // 8192 elements per batch
-constexpr int kCap = 4096;                     // LDS candidate capacity
-constexpr int kWaveCap = kCap / kSelWaves;     // per-wave share of it during the streaming pass
+constexpr int kLaneCap = 16;                   // candidate slots per lane during the streaming pass
+constexpr int kWaveSlots = kLaneCap * 64;      // a wave's slots: slot s of lane l at s * 64 + l
+constexpr int kCap = kSelWaves * kWaveSlots;   // LDS candidate capacity (8192)
 constexpr int kMaxTopK = 1024;
 constexpr int kRaceChunk = 16384;              // vocabulary chunk of the dense race kernels
 
@@ -52,6 +53,27 @@ struct PosRecord {
     int64_t race;   // winner of this position's race (valid unless kFlagDense)
 };
 static_assert(sizeof(PosRecord) == 32, "record layout");
+
+// Records cross workgroups (and XCDs) through device-scope atomic stores and loads, which the gfx950 backend
+// performs at the device's coherence point (sc1) rather than in an XCD's own L2. That keeps them out of the L2
+// write-back a release fence would force on every position.
+__device__ __forceinline__ void store_record(PosRecord* dst, const PosRecord& r) {
+    uint64_t w[4];
+    __builtin_memcpy(w, &r, sizeof(w));
+    uint64_t* d = reinterpret_cast<uint64_t*>(dst);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) __hip_atomic_store(d + i, w[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ PosRecord load_record(const PosRecord* src) {
+    uint64_t w[4];
+    const uint64_t* s = reinterpret_cast<const uint64_t*>(src);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = __hip_atomic_load(s + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    PosRecord r;
+    __builtin_memcpy(&r, w, sizeof(w));
+    return r;
+}
 
 struct SelArgs {
     const void* logits;
@@ -89,25 +111,64 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 // already executes them in order).
 __device__ __forceinline__ void compiler_fence_s() { asm volatile("" ::: "memory"); }
 
+// Wave reductions through DPP (no LDS round trips): rotations by 8, 4, 2 and 1 inside each 16-lane row leave
+// every lane with its row's result; row_bcast:15 folds row 0 into row 1 and row 2 into row 3, row_bcast:31 folds
+// rows 0-1 into rows 2-3, so lane 63 holds the wave's result, which readlane hands to every lane. Lanes of rows
+// a broadcast does not write get `old`: the identity for a sum, the lane's own value for a max.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t src) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(src), CTRL, ROWS, 0xf, false));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    auto step = [](float x, float y) { return x + y; };
+    v = step(v, __uint_as_float(dpp_u32<0x128, 0xf>(0u, __float_as_uint(v))));   // row_ror:8
+    v = step(v, __uint_as_float(dpp_u32<0x124, 0xf>(0u, __float_as_uint(v))));   // row_ror:4
+    v = step(v, __uint_as_float(dpp_u32<0x122, 0xf>(0u, __float_as_uint(v))));   // row_ror:2
+    v = step(v, __uint_as_float(dpp_u32<0x121, 0xf>(0u, __float_as_uint(v))));   // row_ror:1
+    v = step(v, __uint_as_float(dpp_u32<0x142, 0xa>(0u, __float_as_uint(v))));   // row_bcast:15
+    v = step(v, __uint_as_float(dpp_u32<0x143, 0xc>(0u, __float_as_uint(v))));   // row_bcast:31
+    return __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(v)), 63)));
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), o)));
-    return v;
+    v = max(v, dpp_u32<0x128, 0xf>(v, v));
+    v = max(v, dpp_u32<0x124, 0xf>(v, v));
+    v = max(v, dpp_u32<0x122, 0xf>(v, v));
+    v = max(v, dpp_u32<0x121, 0xf>(v, v));
+    v = max(v, dpp_u32<0x142, 0xa>(v, v));
+    v = max(v, dpp_u32<0x143, 0xc>(v, v));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+    v |= dpp_u32<0x128, 0xf>(v, v);
+    v |= dpp_u32<0x124, 0xf>(v, v);
+    v |= dpp_u32<0x122, 0xf>(v, v);
+    v |= dpp_u32<0x121, 0xf>(v, v);
+    v |= dpp_u32<0x142, 0xa>(v, v);
+    v |= dpp_u32<0x143, 0xc>(v, v);
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+    const uint64_t o = (static_cast<uint64_t>(dpp_u32<CTRL, ROWS>(hi, hi)) << 32) | dpp_u32<CTRL, ROWS>(lo, lo);
+    return v > o ? v : o;
 }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t w = __shfl_xor(v, o);
-        v = v > w ? v : w;
-    }
-    return v;
+    v = dpp_max_u64<0x128, 0xf>(v);
+    v = dpp_max_u64<0x124, 0xf>(v);
+    v = dpp_max_u64<0x122, 0xf>(v);
+    v = dpp_max_u64<0x121, 0xf>(v);
+    v = dpp_max_u64<0x142, 0xa>(v);
+    v = dpp_max_u64<0x143, 0xc>(v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), 63));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), 63));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
 // Inclusive prefix sum over the wave.
@@ -177,12 +238,14 @@ __device__ __forceinline__ uint32_t wave_merge_top(uint32_t a, uint32_t b) {
     return v;
 }
 
-// The 64 largest keys of a list of n keys, sorted descending across the wave (key 0 past a shorter list).
-__device__ uint32_t wave_top64(const uint32_t* keys, int n) {
+// The 64 largest keys of a wave's per-lane lists (lane l holds lcnt keys at keys[s * 64 + l], s < lcnt;
+// max_cnt is the wave's largest lcnt), sorted descending across the wave (key 0 past fewer than 64 keys).
+// A slot row whose largest key cannot enter is skipped.
+__device__ uint32_t wave_top64_slots(const uint32_t* keys, int lcnt, int max_cnt) {
     const int l = lane_id();
-    uint32_t top = wave_sort_desc(l < n ? keys[l] : 0u);
-    for (int c0 = 64; c0 < n; c0 += 64) {
-        const uint32_t k = c0 + l < n ? keys[c0 + l] : 0u;
+    uint32_t top = wave_sort_desc(0 < lcnt ? keys[l] : 0u);
+    for (int s = 1; s < max_cnt; ++s) {
+        const uint32_t k = s < lcnt ? keys[s * 64 + l] : 0u;
         const uint32_t floor_key = static_cast<uint32_t>(__shfl(static_cast<int>(top), 63));
         if (__ballot(k > floor_key) == 0ull) continue;
         top = wave_merge_top(top, wave_sort_desc(k));
@@ -479,11 +542,10 @@ __device__ __forceinline__ void wave_pick_bin(const uint32_t* hist, uint32_t ran
     rem = static_cast<uint32_t>(__shfl(static_cast<int>(found_rem), src));
 }
 
-// rank-th largest (1-based) key over n_lists lists (list w at keys + w * stride, counts[w] keys), by one wave
-// alone with its own 256-bin histogram: four 8-bit radix passes, no workgroup barrier. LDS executes one wave's
-// accesses in order; the fences keep the compiler from reordering them. rank must not exceed the total count.
-__device__ uint32_t wave_radix_select_lists(const uint32_t* keys, int stride, const int* counts, int n_lists,
-                                            int rank, uint32_t* hist) {
+// rank-th largest (1-based) key of a wave's per-lane lists (as in wave_top64_slots), by the wave alone with its
+// own 256-bin histogram: four 8-bit radix passes, no workgroup barrier. LDS executes one wave's accesses in
+// order; the fences keep the compiler from reordering them. rank must not exceed the wave's key count.
+__device__ uint32_t wave_radix_select_slots(const uint32_t* keys, int lcnt, int max_cnt, int rank, uint32_t* hist) {
     const int l = lane_id();
     uint32_t prefix = 0u, mask = 0u;
     uint32_t remaining = static_cast<uint32_t>(rank);
@@ -493,11 +555,9 @@ __device__ uint32_t wave_radix_select_lists(const uint32_t* keys, int stride, co
 #pragma unroll
         for (int i = 0; i < 4; ++i) hist[4 * l + i] = 0u;
         compiler_fence_s();
-        for (int w = 0; w < n_lists; ++w) {
-            const uint32_t* list = keys + w * stride;
-            const int n = counts[w];
-            for (int i = l; i < n; i += 64) {
-                const uint32_t key = list[i];
+        for (int s = 0; s < max_cnt; ++s) {
+            if (s < lcnt) {
+                const uint32_t key = keys[s * 64 + l];
                 if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
             }
         }
@@ -511,10 +571,15 @@ __device__ uint32_t wave_radix_select_lists(const uint32_t* keys, int stride, co
     return prefix;
 }
 
-// rank-th largest (1-based) of the n keys at list[0..n), by one wave (see wave_radix_select_lists).
-__device__ uint32_t wave_radix_select(const uint32_t* list, int n, int rank, uint32_t* hist) {
-    const int counts[1] = {n};
-    return wave_radix_select_lists(list, 0, counts, 1, rank, hist);
+// Integer sum over the wave (every lane gets it), through the DPP reduction of wave_sum's shape.
+__device__ __forceinline__ int wave_sum_i32(int v) {
+    v += static_cast<int>(dpp_u32<0x128, 0xf>(0u, static_cast<uint32_t>(v)));
+    v += static_cast<int>(dpp_u32<0x124, 0xf>(0u, static_cast<uint32_t>(v)));
+    v += static_cast<int>(dpp_u32<0x122, 0xf>(0u, static_cast<uint32_t>(v)));
+    v += static_cast<int>(dpp_u32<0x121, 0xf>(0u, static_cast<uint32_t>(v)));
+    v += static_cast<int>(dpp_u32<0x142, 0xa>(0u, static_cast<uint32_t>(v)));
+    v += static_cast<int>(dpp_u32<0x143, 0xc>(0u, static_cast<uint32_t>(v)));
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
 // Key of a value for selection; NaN padding (past the vocabulary) maps to 0, below every real value.
@@ -702,7 +767,7 @@ __device__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L
         const int64_t lim = min(min(L - 1, static_cast<int64_t>(kd)), a.n_pos - start);   // n stays <= lim
         for (int64_t c0 = 0;; c0 += 64) {
             const int64_t pos = min(start + c0 + lane, a.n_pos - 1);
-            const PosRecord r = a.rec[pos];
+            const PosRecord r = load_record(a.rec + pos);
             const bool stop = (c0 + lane >= lim) || !r.acc;
             const uint64_t bal = __ballot(stop);
             if (bal == 0ull) continue;   // all 64 accepted: the next 64
@@ -752,14 +817,15 @@ __device__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L
     }
 }
 
-// Count a finished position of batch row b: a release add on the row's counter, so the position's record
-// (stored before) is visible to whichever position counts last; that one acquires every record of the row and
-// finishes it. Returns whether this position counted last.
+// Count a finished position of batch row b on the row's counter; the position that counts last finishes the row.
+// Returns whether this position counted last. The caller stored its record with store_record: the wait below
+// holds the add back until those stores are performed at the coherence point, and the finishing workgroup issues
+// its record loads (load_record, also at the coherence point) only after its own add has returned, so it reads
+// every record of the row.
 __device__ __forceinline__ bool count_position(int* counter, int64_t n_positions) {
-    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = before == static_cast<int>(n_positions) - 1;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    return last;
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): every store of this wave has completed
+    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return before == static_cast<int>(n_positions) - 1;
 }
 
 template <int DT, int MODE, bool VEC>
@@ -846,62 +912,74 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         rs.z = block_sum(zz, sh);
         rs.m = mall;
     } else {
-        // ---- one pass: every element >= tau, a lower bound of the K-th largest, joins its wave's candidate list.
-        // tau starts from the first batch: each wave's ceil(K/8)-th largest lane maximum, the smallest over the 8
-        // waves, so at least K elements lie at or above it. After that the pass has no workgroup barrier: a wave
-        // appends to its own list; when the list passes half its capacity the wave takes the exact K-th largest
-        // of its own list (a lower bound of the row's too), raises tau to it, drops what lies below and publishes
-        // the bound to the other waves through one LDS word they read each batch. A wave whose list still
-        // overflows sends the row to the exact path.
+        // ---- one pass: every element >= tau, a lower bound of the K-th largest, joins a candidate list private
+        // to its lane: kLaneCap slots, slot s of lane l of wave w at sh.ckey[w * kWaveSlots + s * 64 + l] (the
+        // index at the same place in sh.cidx). tau starts from the first two batches (see below), a value with at
+        // least K elements at or above it. After that the pass has no workgroup barrier and the append no
+        // cross-lane step. When some lane of a wave has filled three quarters of its slots, the wave raises tau to
+        // a bound of the K-th largest of its own lists (a lower bound of the row's too), drops what lies below and
+        // publishes the bound to the other waves through one LDS word they read each batch. A lane whose list
+        // still overflows sends the row to the exact path.
         const int wave = threadIdx.x >> 6;
         const int lane = lane_id();
-        uint32_t* wkey = sh.ckey + wave * kWaveCap;
-        int32_t* widx = sh.cidx + wave * kWaveCap;
+        uint32_t* wkey = sh.ckey + wave * kWaveSlots;
+        int32_t* widx = sh.cidx + wave * kWaveSlots;
         const int nb = static_cast<int>((a.vocab + kBatch - 1) / kBatch);
         uint32_t tau_key = 0xffffffffu;
         float tau = INFINITY;
-        int wcount = 0;
-        uint32_t hmax = 0u;   // largest key this lane appended
-        bool overflow = false;
+        int lcnt = 0;           // this lane's list length
+        uint32_t hmax = 0u;     // largest key this lane appended
+        bool overflow = false;  // the same on every lane of the wave
 
-        // The K-th largest of this wave's list becomes its bound; entries below it leave the list.
+        // A tighter bound from this wave's lists: one 256-bin histogram of the listed keys at or above tau, the
+        // bins spread over [tau, the wave's largest key]; the lower edge of the bin holding the wave's K-th largest
+        // has at least K listed keys at or above it. Entries below the new bound leave the lists.
         auto refine = [&]() {
-            const uint32_t kth = K <= 64 ? static_cast<uint32_t>(__shfl(static_cast<int>(wave_top64(wkey, wcount)), K - 1))
-                                         : wave_radix_select(wkey, wcount, K, sh.whist[wave]);
-            if (kth > tau_key || tau_key == 0xffffffffu) {
-                tau_key = kth;
-                tau = nvs::key_float(kth);
-                atomicMax(&sh.tau_key, kth);
-            }
-            constexpr int kPer = kWaveCap / 64;
-            uint32_t kk[kPer];
-            int32_t ii[kPer];
+            if (wave_sum_i32(lcnt) < K) return;   // too few keys to bound the K-th largest
+            const int max_cnt = static_cast<int>(wave_max_u32(static_cast<uint32_t>(lcnt)));
+            const uint32_t whi = wave_max_u32(hmax);
+            if (whi > tau_key) {
+                uint32_t* hist = sh.whist[wave];
+                const uint32_t range = whi - tau_key;
+                const int sh_bits = range < 256u ? 0 : 24 - __clz(range);
 #pragma unroll
-            for (int j = 0; j < kPer; ++j) {
-                const int c = lane + 64 * j;
-                kk[j] = c < wcount ? wkey[c] : 0u;
-                ii[j] = c < wcount ? widx[c] : 0;
-            }
-            compiler_fence_s();
-            const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-            int kept = 0;
-#pragma unroll
-            for (int j = 0; j < kPer; ++j) {
-                const bool keep = kk[j] != 0u && kk[j] >= tau_key;
-                const uint64_t bal = __ballot(keep);
-                if (keep) {
-                    const int pos = kept + __popcll(bal & below);
-                    wkey[pos] = kk[j];
-                    widx[pos] = ii[j];
+                for (int i = 0; i < 4; ++i) hist[4 * lane + i] = 0u;
+                compiler_fence_s();
+                for (int s = 0; s < max_cnt; ++s) {
+                    if (s < lcnt) {
+                        const uint32_t k = wkey[s * 64 + lane];
+                        if (k >= tau_key) atomicAdd(&hist[(k - tau_key) >> sh_bits], 1u);
+                    }
                 }
-                kept += __popcll(bal);
+                compiler_fence_s();
+                uint32_t b, r;
+                wave_pick_bin(hist, static_cast<uint32_t>(K), b, r);
+                compiler_fence_s();
+                if (b < 256u && b > 0u) {
+                    const uint32_t kb = tau_key + (b << sh_bits);
+                    tau_key = kb;
+                    tau = nvs::key_float(kb);
+                    atomicMax(&sh.tau_key, kb);
+                }
+            }
+            // each lane compacts its own list in place (slot kept <= s: every read precedes the write over it)
+            compiler_fence_s();
+            int kept = 0;
+            for (int s = 0; s < lcnt; ++s) {
+                const uint32_t k = wkey[s * 64 + lane];
+                const int32_t ix = widx[s * 64 + lane];
+                if (k >= tau_key) {
+                    wkey[kept * 64 + lane] = k;
+                    widx[kept * 64 + lane] = ix;
+                    ++kept;
+                }
             }
             compiler_fence_s();
-            wcount = kept;
+            lcnt = kept;
         };
 
         // Filter one batch. Most batches hold no element at or above tau in the whole wave: one max, one compare,
-        // one ballot. Otherwise the passing values are appended to the wave's list.
+        // one ballot. Otherwise each lane with a passing value appends it to its own list.
         auto filter = [&](float (&sv)[kVpt], int bi) {   // scales the buffer in place (it is reloaded next)
             const int64_t e0 = static_cast<int64_t>(bi) * kBatch;
             if (!unit_temp) {
@@ -911,23 +989,6 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             if (e0 + kBatch > a.vocab) {   // the last, partial batch: elements past the row are NaN
 #pragma unroll
                 for (int vi = 0; vi < kVpt; ++vi) sv[vi] = val_index<DT>(e0, vi) < a.vocab ? sv[vi] : NAN;
-            }
-            if (bi == 0) {
-                uint32_t tmax = 0u;
-#pragma unroll
-                for (int vi = 0; vi < kVpt; ++vi) tmax = max(tmax, sel_key(sv[vi]));
-                const int rw = (K + kSelWaves - 1) / kSelWaves;
-                uint32_t bound = 0u;
-                if (rw <= 64) {
-                    const uint32_t sorted = wave_sort_desc(tmax);
-                    bound = static_cast<uint32_t>(__shfl(static_cast<int>(sorted), rw - 1));
-                }
-                if (lane == 0) sh.ured[wave] = bound;
-                __syncthreads();
-                uint32_t b = 0xffffffffu;
-                for (int w = 0; w < kSelWaves; ++w) b = min(b, sh.ured[w]);
-                tau_key = b;
-                tau = (b == 0u) ? -INFINITY : nvs::key_float(b);   // NaN never passes a >= test
             }
             const uint32_t shared_key = __hip_atomic_load(&sh.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             // every path reads the whole buffer first, so its loads are complete before the buffer is reloaded
@@ -939,54 +1000,84 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                 tau_key = shared_key;
                 tau = nvs::key_float(shared_key);
             }
-            // each lane marks its passing values in a bitmask and writes them after its wave prefix of the counts
-            uint32_t pass = 0u;
+            if (hi >= tau) {
 #pragma unroll
-            for (int vi = 0; vi < kVpt; ++vi) pass |= (sv[vi] >= tau ? 1u : 0u) << vi;
-            const int c = __popc(pass);
-            const int incl = wave_scan_incl_dpp(c);
-            const int total = __builtin_amdgcn_readlane(incl, 63);
-            if (wcount + total > kWaveCap) {
+                for (int vi = 0; vi < kVpt; ++vi) {
+                    if (sv[vi] >= tau) {
+                        const uint32_t key = nvs::float_key(sv[vi]);
+                        // a full list overwrites its last slot; the overflow test below then sends the row to the
+                        // exact path
+                        const int s = min(lcnt, kLaneCap - 1);
+                        wkey[s * 64 + lane] = key;
+                        widx[s * 64 + lane] = static_cast<int32_t>(val_index<DT>(e0, vi));
+                        hmax = max(hmax, key);
+                        ++lcnt;
+                    }
+                }
+            }
+            if (__ballot(lcnt > kLaneCap * 3 / 4) == 0ull) return;
+            if (__ballot(lcnt > kLaneCap) != 0ull) {
                 overflow = true;   // the exact path re-reads the row
                 return;
             }
-            int pos = wcount + incl - c;
-#pragma unroll
-            for (int vi = 0; vi < kVpt; ++vi) {
-                if ((pass >> vi) & 1u) {
-                    const uint32_t key = nvs::float_key(sv[vi]);
-                    wkey[pos] = key;
-                    widx[pos] = static_cast<int32_t>(val_index<DT>(e0, vi));
-                    hmax = max(hmax, key);
-                    ++pos;
-                }
-            }
-            wcount += total;
-            if (wcount > kWaveCap / 2 && wcount >= K) refine();
+            refine();
         };
 
         // Three register buffers in a ring, unrolled so no values are copied: while one batch is filtered the
-        // next two are in flight.
+        // next two are in flight. The loads are unconditional: a load guarded by a branch is sunk by the compiler
+        // to its use, which leaves nothing in flight during the filter. Past the row every lane's address clamps
+        // to the row's last piece (one cache line, never used).
         float ra[kVpt], rb[kVpt], rc[kVpt];
         load_vals<DT, VEC, false>(row, 0, a.vocab, ra);
-        if (nb > 1) load_vals<DT, VEC, false>(row, kBatch, a.vocab, rb);
+        load_vals<DT, VEC, false>(row, kBatch, a.vocab, rb);
         load_decision();   // after the draft token, behind the first two batches
+        {
+            // The first bound: each lane's largest value over the first two batches, each wave's ceil(K/8)-th
+            // largest lane maximum, the smallest of those over the 8 waves. Every wave has ceil(K/8) lanes holding
+            // a value at or above it, so at least K elements of the row do.
+            // The largest scaled value is the largest raw value divided by a positive temperature (division
+            // rounds monotonically), the smallest one for a negative temperature.
+            float mx = -INFINITY, mn = INFINITY;
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) {
+                const bool ina = val_index<DT>(0, vi) < a.vocab, inb = val_index<DT>(kBatch, vi) < a.vocab;
+                mx = fmaxf(mx, fmaxf(ina ? ra[vi] : -INFINITY, inb ? rb[vi] : -INFINITY));
+                mn = fminf(mn, fminf(ina ? ra[vi] : INFINITY, inb ? rb[vi] : INFINITY));
+            }
+            // A lane with nothing (or only -inf) counts as holding nothing: that can only lower the bound.
+            const float ext = scale_logit(temp < 0.f ? mn : mx, temp, unit_temp);
+            const uint32_t tmax = (ext == -INFINITY || ext != ext) ? 0u : sel_key(ext);
+            const int rw = (K + kSelWaves - 1) / kSelWaves;
+            uint32_t bound = 0u;
+            if (rw <= 64) {
+                const uint32_t sorted = wave_sort_desc(tmax);
+                bound = static_cast<uint32_t>(__shfl(static_cast<int>(sorted), rw - 1));
+            }
+            if (lane == 0) sh.ured[wave] = bound;
+            __syncthreads();
+            uint32_t b = 0xffffffffu;
+            for (int w = 0; w < kSelWaves; ++w) b = min(b, sh.ured[w]);
+            tau_key = b;
+            tau = (b == 0u) ? -INFINITY : nvs::key_float(b);   // NaN never passes a >= test
+        }
         for (int bi = 0;;) {
-            if (bi + 2 < nb) load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rc);
+            load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rc);
             filter(ra, bi);
             if (++bi >= nb) break;
-            if (bi + 2 < nb) load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, ra);
+            load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, ra);
             filter(rb, bi);
             if (++bi >= nb) break;
-            if (bi + 2 < nb) load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rb);
+            load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rb);
             filter(rc, bi);
             if (++bi >= nb) break;
         }
-        if (overflow) wcount = kWaveCap + 1;
+        lcnt = min(lcnt, kLaneCap);   // past it only when the row goes to the exact path
         const uint32_t wave_hi = wave_max_u32(hmax);
+        const int wave_total = wave_sum_i32(lcnt);
+        const int max_cnt = static_cast<int>(wave_max_u32(static_cast<uint32_t>(lcnt)));
         if (lane == 0) {
-            sh.wcount[wave] = min(wcount, kWaveCap);
-            if (wcount > kWaveCap) sh.overflow = 1;
+            sh.wcount[wave] = wave_total;
+            if (overflow) sh.overflow = 1;
             sh.wlo[wave] = tau_key;
             sh.wmax[wave] = wave_hi;
         }
@@ -1018,10 +1109,11 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             }
             const uint32_t range = hi - lo;
             shift = range < 256u ? 0 : 24 - __clz(range);
-            const int cnt = sh.wcount[wave];
-            for (int i = lane; i < cnt; i += 64) {
-                const uint32_t key = wkey[i];
-                if (key >= lo) atomicAdd(&sh.hist[(key - lo) >> shift], 1u);
+            for (int s = 0; s < max_cnt; ++s) {
+                if (s < lcnt) {
+                    const uint32_t key = wkey[s * 64 + lane];
+                    if (key >= lo) atomicAdd(&sh.hist[(key - lo) >> shift], 1u);
+                }
             }
             __syncthreads();
             wave_pick_bin(sh.hist, static_cast<uint32_t>(rank), bin, bin_rank);
@@ -1032,10 +1124,10 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             fast = picked && n_top <= kTopCap;
             if (fast) {
                 const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-                for (int c0 = 0; c0 < cnt; c0 += 64) {
-                    const int i = c0 + lane;
-                    const uint32_t key = i < cnt ? wkey[i] : 0u;
-                    const bool in = i < cnt && key >= lo;
+                for (int s = 0; s < max_cnt; ++s) {
+                    const int i = s * 64 + lane;
+                    const uint32_t key = s < lcnt ? wkey[i] : 0u;
+                    const bool in = s < lcnt && key >= lo;
                     const uint32_t d = (key - lo) >> shift;
                     const bool take = in && d >= bin;
                     const uint64_t bal = __ballot(take);
@@ -1139,7 +1231,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                                                    : int64_t{0};
                         }
                         r.race = winner;
-                        a.rec[t] = r;
+                        store_record(a.rec + t, r);
                         if (sh.found) {
                             const int64_t L_eff = min(max(L, int64_t{1}), static_cast<int64_t>(kd) + 1);
                             sh.last = count_position(&a.counters[b], L_eff) ? 1 : 0;
@@ -1155,29 +1247,26 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             record_done = true;
         } else {
         if (!exact) {
-            // the per-wave lists, one after another
+            // the lanes' lists, one after another (wave by wave, lane by lane), at the front of the buffer
             int off = 0, total = 0;
             for (int w = 0; w < kSelWaves; ++w) {
                 off += (w < wave) ? sh.wcount[w] : 0;
                 total += sh.wcount[w];
             }
-            const int cnt = sh.wcount[wave];
-            constexpr int kPer = kWaveCap / 64;
-            uint32_t kk[kPer];
-            int32_t ii[kPer];
+            off += wave_scan_incl_dpp(lcnt) - lcnt;
+            uint32_t kk[kLaneCap];
+            int32_t ii[kLaneCap];
 #pragma unroll
-            for (int j = 0; j < kPer; ++j) {
-                const int c = lane_id() + 64 * j;
-                kk[j] = c < cnt ? wkey[c] : 0u;
-                ii[j] = c < cnt ? widx[c] : 0;
+            for (int s = 0; s < kLaneCap; ++s) {
+                kk[s] = s < lcnt ? wkey[s * 64 + lane] : 0u;
+                ii[s] = s < lcnt ? widx[s * 64 + lane] : 0;
             }
             __syncthreads();
 #pragma unroll
-            for (int j = 0; j < kPer; ++j) {
-                const int c = lane_id() + 64 * j;
-                if (c < cnt) {
-                    sh.ckey[off + c] = kk[j];
-                    sh.cidx[off + c] = ii[j];
+            for (int s = 0; s < kLaneCap; ++s) {
+                if (s < lcnt) {
+                    sh.ckey[off + s] = kk[s];
+                    sh.cidx[off + s] = ii[s];
                 }
             }
             if (threadIdx.x == 0) sh.count = total;
@@ -1293,7 +1382,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                                        : int64_t{0};
             }
             r.race = winner;
-            a.rec[t] = r;
+            store_record(a.rec + t, r);
             // count the position; the row's last position to arrive finishes the row
             if (sh.found) {
                 const int64_t L_eff = min(max(L, int64_t{1}), static_cast<int64_t>(kd) + 1);
