@@ -11,6 +11,7 @@ top-k 64), against the one read of the [512, V] logits it must make; and the tor
 attention (the oracle, the reference's CPU path) on the host cores as a reported baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-baseline on|off] [--sampler on|off]
+                       [--copy-probe on|off]
 """
 import argparse
 import json
@@ -21,6 +22,14 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "verify-attn µs/layer & HBM GB/s (% of 8 TB/s) at B=64, 8 q, 3k ctx"
+
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (one counter per run), each scaled
+# by what the counter reads for the 1 GiB copy probe (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); the runs and their
+# numbers are in profiles/hbm_traffic_pmc_verify_attention_and_spec_accept.md. Re-measure after a kernel change.
+MEASURED_TRAFFIC = {
+    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200": 789_786_632,
+    "spec_accept_b64_k7_v151936_fp32_topk64": 320_000_031,
+}
 
 
 def log(msg: str) -> None:
@@ -133,7 +142,22 @@ def sampler_bench(args, dev):
     log(f"[bench] fused sampler: {ms * 1e3:.1f} us, {gbs:.0f} GB/s = {100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
     return {"workload": "spec_accept_b64_k7_v151936_fp32_topk64", "us": round(ms * 1e3, 2),
             "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": alg,
+            "traffic": MEASURED_TRAFFIC["spec_accept_b64_k7_v151936_fp32_topk64"],
+            "kernel": "select_kernel<f32, accept> (one launch per call)",
             "mean_accepted": round(float(n.float().mean()), 3)}
+
+
+def copy_probe(args, dev):
+    """A plain 1 GiB device-to-device copy: the HBM rate a streaming kernel can reach on this box, and, under
+    rocprofv3 --pmc, the known-size kernel that scales FETCH_SIZE / WRITE_SIZE to bytes."""
+    import torch
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = time_gpu(lambda: dst.copy_(src), max(5, args.steps // 10), 2)
+    gbs = 2 * n / (ms * 1e-3) / 1e9
+    log(f"[bench] 1 GiB copy: {ms * 1e3:.1f} us, {gbs:.0f} GB/s read+write")
+    return {"bytes_read": n, "bytes_written": n, "us": round(ms * 1e3, 2), "GBs_read_plus_write": round(gbs, 1)}
 
 
 def cpu_baseline(case):
@@ -166,6 +190,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--sampler", choices=["on", "off"], default="on")
+    ap.add_argument("--copy-probe", choices=["on", "off"], default="off",
+                    help="also time a plain 1 GiB device copy (the counter scale for rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the verify hot path runs on one GPU's share and this build has no "
@@ -186,7 +212,9 @@ def main():
     extra = {"c2": launch_bound_bench(args, dev)}
     if args.sampler == "on":
         extra["sampler"] = sampler_bench(args, dev)
-    cpu = cpu_baseline(case) if args.cpu_baseline == "on" else None
+    if args.copy_probe == "on":
+        extra["copy_probe"] = copy_probe(args, dev)
+    cpu =cpu_baseline(case) if args.cpu_baseline == "on" else None
 
     result = {
         "metric": METRIC,
@@ -207,9 +235,10 @@ def main():
         "us_per_layer": round(ms * 1e3, 2),
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": MEASURED_TRAFFIC["verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200"],
                      "bytes_per_launch": nbytes,
-                     "kernel": "attn_split_kernel + attn_combine_kernel (one paged_attention call)"},
+                     "kernel": "attn_split_kernel (batch 64 runs unsplit: one launch per paged_attention call)"},
         "mfma_tflops_useful": round(flops / (ms * 1e-3) / 1e12, 2),
         "cpu_baseline": cpu,
         "extra": extra,
