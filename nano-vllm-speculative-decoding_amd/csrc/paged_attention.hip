@@ -15,14 +15,16 @@
 //   fp32 partial (O, max, sum) and attn_combine_kernel merges them with the log-sum-exp rule.
 //
 // Per chunk of 32 keys, per wave (lane l: packed row nl = l % 32, half gi = l / 32):
-//   S^T[32 keys x 32 rows] = K[32 x 128] . Q^T      8 x v_mfma_f32_32x32x16_bf16, K loaded straight from HBM
-//                                                    into the A-operand layout (lane = key, 8 dims per half)
+//   load    K and V rows of the chunk with coalesced streaming 16-byte loads (4 keys x 256 B per instruction,
+//           page and block id clamped into range) and stage them into the wave's padded LDS tiles; the loads of
+//           chunk c + 4 (the wave's next chunk) are issued right after, so they are in flight during the math
+//   S^T[32 keys x 32 rows] = K[32 x 128] . Q^T      8 x v_mfma_f32_32x32x16_bf16, K read from the LDS tile in the
+//                                                    A-operand layout, Q from the LDS query tile
 //   online softmax in fp32 with exp2 (scale * log2 e folded into one multiply); each lane owns one packed row,
 //   the two halves of a row are merged with one cross-lane exchange
 //   O^T[128 x 32] += V^T[128 x 32 keys] . P^T       8 x v_mfma_f32_32x32x16_bf16; P rounded to bf16 as the B
-//                                                    operand straight from the S accumulators; V transposed
-//                                                    through a wave-private LDS tile
-// K and V of the next chunk are loaded into registers while the current one is processed.
+//                                                    operand straight from the S accumulators; V^T gathered from
+//                                                    the LDS tile with 16-bit reads
 #include "nvs_common.hpp"
 
 #include <cmath>

@@ -142,16 +142,6 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
 }
 
-__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
-    v |= dpp_u32<0x128, 0xf>(v, v);
-    v |= dpp_u32<0x124, 0xf>(v, v);
-    v |= dpp_u32<0x122, 0xf>(v, v);
-    v |= dpp_u32<0x121, 0xf>(v, v);
-    v |= dpp_u32<0x142, 0xa>(v, v);
-    v |= dpp_u32<0x143, 0xc>(v, v);
-    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
-}
-
 template <int CTRL, int ROWS>
 __device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
     const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
@@ -224,40 +214,11 @@ __device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v) {
     return v;
 }
 
-// The 64 largest of two descending wave-sorted lists (one value per lane each), sorted descending: the larger
-// of a[i] and b[63 - i] forms a bitonic sequence holding the 64 largest, which a bitonic merge sorts.
-__device__ __forceinline__ uint32_t wave_merge_top(uint32_t a, uint32_t b) {
-    const int l = lane_id();
-    const uint32_t r = static_cast<uint32_t>(__shfl(static_cast<int>(b), 63 - l));
-    uint32_t v = max(a, r);
-#pragma unroll
-    for (int stride = 32; stride > 0; stride >>= 1) {
-        const uint32_t w = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), stride));
-        v = ((l & stride) == 0) ? max(v, w) : min(v, w);
-    }
-    return v;
-}
-
-// The 64 largest keys of a wave's per-lane lists (lane l holds lcnt keys at keys[s * 64 + l], s < lcnt;
-// max_cnt is the wave's largest lcnt), sorted descending across the wave (key 0 past fewer than 64 keys).
-// A slot row whose largest key cannot enter is skipped.
-__device__ uint32_t wave_top64_slots(const uint32_t* keys, int lcnt, int max_cnt) {
-    const int l = lane_id();
-    uint32_t top = wave_sort_desc(0 < lcnt ? keys[l] : 0u);
-    for (int s = 1; s < max_cnt; ++s) {
-        const uint32_t k = s < lcnt ? keys[s * 64 + l] : 0u;
-        const uint32_t floor_key = static_cast<uint32_t>(__shfl(static_cast<int>(top), 63));
-        if (__ballot(k > floor_key) == 0ull) continue;
-        top = wave_merge_top(top, wave_sort_desc(k));
-    }
-    return top;
-}
-
 struct SelShared {
     uint32_t ckey[kCap];
     int32_t cidx[kCap];
     uint32_t hist[256];
-    uint32_t whist[kSelWaves][256];  // per-wave radix-select histograms of the streaming pass
+    uint32_t whist[kSelWaves][256];  // per-wave bound-refinement histograms; afterwards the threshold bin's keys
     uint32_t tau_key;                // workgroup-wide lower bound of the K-th largest key (only ever raised)
     uint32_t sortbuf[kMaxTopK];
     float fred[kSelWaves];
@@ -540,35 +501,6 @@ __device__ __forceinline__ void wave_pick_bin(const uint32_t* hist, uint32_t ran
     const int src = who ? static_cast<int>(__ffsll(static_cast<long long>(who))) - 1 : 0;
     bin = static_cast<uint32_t>(__shfl(found_bin, src));
     rem = static_cast<uint32_t>(__shfl(static_cast<int>(found_rem), src));
-}
-
-// rank-th largest (1-based) key of a wave's per-lane lists (as in wave_top64_slots), by the wave alone with its
-// own 256-bin histogram: four 8-bit radix passes, no workgroup barrier. LDS executes one wave's accesses in
-// order; the fences keep the compiler from reordering them. rank must not exceed the wave's key count.
-__device__ uint32_t wave_radix_select_slots(const uint32_t* keys, int lcnt, int max_cnt, int rank, uint32_t* hist) {
-    const int l = lane_id();
-    uint32_t prefix = 0u, mask = 0u;
-    uint32_t remaining = static_cast<uint32_t>(rank);
-#pragma unroll 1
-    for (int pass = 0; pass < 4; ++pass) {
-        const int shift = 24 - 8 * pass;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) hist[4 * l + i] = 0u;
-        compiler_fence_s();
-        for (int s = 0; s < max_cnt; ++s) {
-            if (s < lcnt) {
-                const uint32_t key = keys[s * 64 + l];
-                if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-            }
-        }
-        compiler_fence_s();
-        uint32_t digit;
-        wave_pick_bin(hist, remaining, digit, remaining);
-        prefix |= digit << shift;
-        mask |= 255u << shift;
-        compiler_fence_s();
-    }
-    return prefix;
 }
 
 // Integer sum over the wave (every lane gets it), through the DPP reduction of wave_sum's shape.
@@ -1060,16 +992,28 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             tau_key = b;
             tau = (b == 0u) ? -INFINITY : nvs::key_float(b);   // NaN never passes a >= test
         }
-        for (int bi = 0;;) {
-            load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rc);
-            filter(ra, bi);
-            if (++bi >= nb) break;
-            load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, ra);
-            filter(rb, bi);
-            if (++bi >= nb) break;
-            load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rb);
-            filter(rc, bi);
-            if (++bi >= nb) break;
+        if constexpr (VEC) {
+            for (int bi = 0;;) {
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rc);
+                filter(ra, bi);
+                if (++bi >= nb) break;
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, ra);
+                filter(rb, bi);
+                if (++bi >= nb) break;
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rb);
+                filter(rc, bi);
+                if (++bi >= nb) break;
+            }
+        } else {
+            // element loads need an address per value: two buffers, one batch in flight, keep it in registers
+            for (int bi = 0;;) {
+                filter(ra, bi);
+                if (++bi >= nb) break;
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 1) * kBatch, a.vocab, ra);
+                filter(rb, bi);
+                if (++bi >= nb) break;
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 1) * kBatch, a.vocab, rb);
+            }
         }
         lcnt = min(lcnt, kLaneCap);   // past it only when the row goes to the exact path
         const uint32_t wave_hi = wave_max_u32(hmax);

@@ -5,6 +5,7 @@ within fp32 rounding (rtol 1e-5, atol 1e-7) with identical zero patterns; trunca
 On a mismatch the decision margin is printed: a flip is only legitimate when u*q and p (or two race scores)
 agree to a few ulps, because the kernel's exp and summation order differ from torch's CPU ones.
 """
+import dataclasses
 import json
 import math
 import pathlib
@@ -187,6 +188,61 @@ def test_fused_accept_is_bit_exact(device, name, kwargs):
     assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want)
     assert torch.equal(tail_got, tail_want)
     print(f"{name}: accepted {n_got.float().mean():.2f} of {case.drafts.shape[1]} on average")
+
+
+def ordered_logits(case, kind):
+    """Target logits laid out against the streaming pass's first bound (taken from the first two 8192-element
+    batches of a row): ascending rows put every large value after it (the lists fill and the row takes the exact
+    path), descending rows put them all inside it, a rising trend makes the waves refine their bound mid-row, and
+    quantised bf16 ramps add massive ties."""
+    T, V = case.logits.shape
+    ramp = torch.arange(V, dtype=torch.float32) / V
+    rows = torch.arange(T, dtype=torch.float32)[:, None] * 1e-3
+    g = torch.Generator().manual_seed(21)
+    if kind == "ascending":
+        return ramp[None, :] * 12.0 - 6.0 + rows
+    if kind == "descending":
+        return ramp.flip(0)[None, :] * 12.0 - 6.0 + rows
+    if kind == "rising_trend":
+        return torch.randn(T, V, generator=g) + 6.0 * ramp[None, :]
+    if kind == "bf16_ramp_ties":
+        return (torch.round((ramp[None, :] * 12.0 - 6.0 + rows) * 4) / 4).to(torch.bfloat16)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["ascending", "descending", "rising_trend", "bf16_ramp_ties"])
+def test_fused_accept_bound_refinement_and_exact_fallback(device, kind):
+    log_case(f"fused accept ordered logits {kind}")
+    base = wl.sampler_case(8, 7, 151936, draft_probs_fn=draft_probs)
+    case = dataclasses.replace(base, logits=ordered_logits(base, kind))
+    n_got, tail_got = run_fused(case, device)
+    n_want, tail_want = run_oracle(case)
+    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want)
+    assert torch.equal(tail_got, tail_want)
+
+
+@pytest.mark.parametrize("top_k", [200, 700])
+def test_fused_accept_large_top_k(device, top_k):
+    """top-k 200 still fits the short threshold list; 700 exceeds the first bound's reach (ceil(K/8) > 64 lanes per
+    wave) and every row takes the exact path."""
+    log_case(f"fused accept top_k {top_k}")
+    case = wl.sampler_case(8, 7, 151936, top_k=top_k, draft_probs_fn=draft_probs)
+    n_got, tail_got = run_fused(case, device)
+    n_want, tail_want = run_oracle(case)
+    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want)
+    assert torch.equal(tail_got, tail_want)
+
+
+@pytest.mark.parametrize("kind", ["ascending", "rising_trend"])
+def test_probs_on_ordered_logits(device, kind):
+    log_case(f"probs ordered logits {kind}")
+    base = wl.sampler_case(4, 1, 151936, draft_probs_fn=draft_probs)   # 8 rows: 2 positions x 4 parameter rows
+    logits = ordered_logits(base, kind).reshape(4, 2, -1)
+    st, (t, k, p, mk, hp) = sampling([(1.0, 64, 1.0), (0.8, 5, 1.0), (1.0, 200, 1.0), (1.3, 64, 0.8)], device)
+    want = ref.probs_from_logits(logits, t, k, p, mk, hp)
+    got = ns.probs_from_logits(logits.to(device), st).cpu()
+    assert torch.equal(got > 0, want > 0)
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-7)
 
 
 def test_fused_accept_repeats_and_replays_in_a_graph(device):
