@@ -962,7 +962,8 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         float ra[kVpt], rb[kVpt], rc[kVpt];
         load_vals<DT, VEC, false>(row, 0, a.vocab, ra);
         load_vals<DT, VEC, false>(row, kBatch, a.vocab, rb);
-        load_decision();   // after the draft token, behind the first two batches
+        if constexpr (VEC) load_vals<DT, VEC, false>(row, 2 * kBatch, a.vocab, rc);   // in flight during the bound
+        load_decision();   // after the draft token, behind the first batches
         {
             // The first bound: each lane's largest value over the first two batches, each wave's ceil(K/8)-th
             // largest lane maximum, the smallest of those over the 8 waves. Every wave has ceil(K/8) lanes holding
@@ -993,15 +994,16 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             tau = (b == 0u) ? -INFINITY : nvs::key_float(b);   // NaN never passes a >= test
         }
         if constexpr (VEC) {
+            // each buffer is reloaded with the batch three ahead as soon as it is filtered
             for (int bi = 0;;) {
-                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rc);
                 filter(ra, bi);
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 3) * kBatch, a.vocab, ra);
                 if (++bi >= nb) break;
-                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, ra);
                 filter(rb, bi);
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 3) * kBatch, a.vocab, rb);
                 if (++bi >= nb) break;
-                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 2) * kBatch, a.vocab, rb);
                 filter(rc, bi);
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 3) * kBatch, a.vocab, rc);
                 if (++bi >= nb) break;
             }
         } else {
