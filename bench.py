@@ -147,6 +147,69 @@ def sampler_bench(args, dev):
             "mean_accepted": round(float(n.float().mean()), 3)}
 
 
+def qk_rope_bench(args, dev):
+    """The fused q/k RMSNorm + rotary + KV store of one batch-64 verify layer (296 tokens, 32/8 heads), against
+    the same sequence as separate torch ops on the GPU (norm q, norm k, rotate both, index the caches)."""
+    import torch
+
+    import nvs_amd.workloads as wl
+    from nvs_amd.layers import qk_norm_rope as nrope
+    case = wl.qk_rope_case(296).to(dev)
+    q, k, v = case.split()
+    q_out = torch.empty_like(q)
+
+    def fused():
+        nrope.qk_norm_rope_store(case.positions, q, k, v, case.q_norm_weight, case.k_norm_weight, case.eps,
+                                 case.table, case.k_cache, case.v_cache, case.slot_mapping, q_out=q_out)
+
+    def rms(x, w):
+        xf = x.to(torch.float32, copy=True)
+        xf.mul_(torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + case.eps))
+        return xf.to(x.dtype).mul_(w)
+
+    def rot(x, cos, sin):
+        x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+    live = torch.nonzero(case.slot_mapping >= 0).flatten()
+    slots = case.slot_mapping[live].long()
+    kc = case.k_cache.view(-1, case.num_kv_heads, case.head_dim)
+    vc = case.v_cache.view(-1, case.num_kv_heads, case.head_dim)
+
+    def torch_ops():
+        cos, sin = case.table[case.positions].unsqueeze(1).chunk(2, dim=-1)
+        qr = rot(rms(q, case.q_norm_weight), cos, sin)
+        kr = rot(rms(k, case.k_norm_weight), cos, sin)
+        kc.index_copy_(0, slots, kr.index_select(0, live))
+        vc.index_copy_(0, slots, v.index_select(0, live))
+        return qr
+
+    # both run as they would inside the verify graphs: 20 calls captured in one HIP graph, timed per call
+    reps = 20
+
+    def graphed(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        return graph
+
+    g_fused, g_torch = graphed(fused), graphed(torch_ops)
+    ms = time_gpu(g_fused.replay, max(10, args.steps // 4), 3) / reps
+    ms_torch = time_gpu(g_torch.replay, max(10, args.steps // 4), 3) / reps
+    b = case.bytes_moved()
+    log(f"[bench] q/k norm + rope + store: {ms * 1e3:.2f} us fused, {ms_torch * 1e3:.2f} us as torch ops "
+        f"(graph replay)")
+    return {"workload": "qk_norm_rope_store_qwen3_8b_296_tokens", "us": round(ms * 1e3, 2),
+            "us_torch_ops": round(ms_torch * 1e3, 2), "bytes": b, "GBs": round(b / (ms * 1e-3) / 1e9, 1),
+            "timing": "HIP graph of 20 calls, per call", "kernel": "qk_norm_rope_store_kernel (one launch)"}
+
+
 def copy_probe(args, dev):
     """A plain 1 GiB device-to-device copy: the HBM rate a streaming kernel can reach on this box, and, under
     rocprofv3 --pmc, the known-size kernel that scales FETCH_SIZE / WRITE_SIZE to bytes."""
@@ -209,7 +272,7 @@ def main():
     dev = torch.device("cuda", 0)
 
     case, ms, nbytes, gbs, flops = attention_bench(args, dev)
-    extra = {"c2": launch_bound_bench(args, dev)}
+    extra = {"c2": launch_bound_bench(args, dev), "qk_norm_rope_store": qk_rope_bench(args, dev)}
     if args.sampler == "on":
         extra["sampler"] = sampler_bench(args, dev)
     if args.copy_probe == "on":

@@ -2,7 +2,8 @@
  * nvs_amd.h -- C ABI of the MI355X (gfx950) target-verify hot path of nano-vllm-speculative-decoding.
  *
  * Two ops live behind this boundary:
- *   1. paged multi-query verify attention (+ the paged KV store that precedes it), and
+ *   1. paged multi-query verify attention (+ the paged KV store, and the fused q/k RMSNorm + RoPE + store, that
+ *      precede it), and
  *   2. the speculative sampler: truncation -> softmax -> rejection test -> residual / bonus race.
  *
  * Every entry point takes plain device pointers, element strides and sizes, plus the HIP stream to launch on
@@ -27,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NVS_ABI_VERSION 1
+#define NVS_ABI_VERSION 2
 
 typedef enum {
     NVS_OK = 0,
@@ -64,6 +65,32 @@ int nvs_store_kvcache(const void* key, int64_t key_row_stride,
                       void* k_cache, void* v_cache, int64_t cache_slots,
                       const int32_t* slot_mapping, int64_t n_tokens,
                       int n_kv_heads, int head_dim, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ q/k norm, RoPE, store
+ * Replaces the sequence between the qkv projection and the attention kernel, in one launch:
+ *   q = q_norm(q); k = k_norm(k); q, k = rotary_emb(positions, q, k)   (nanovllm/models/qwen3.py:82-85;
+ *   RMSNorm.rms_forward nanovllm/layers/layernorm.py:15-24; apply_rotary_emb / RotaryEmbedding.forward
+ *   nanovllm/layers/rotary_embedding.py:6-14,37-47), then store_kvcache(k, v, k_cache, v_cache, slot_mapping)
+ *   (Attention.forward, nanovllm/layers/attention.py:63-64).
+ * With n_heads == 0 and q = q_out = NULL it is the draft model's keys-only path (DFlashDraftModel.store_context_kv,
+ * nanovllm/models/dflash.py:88-96: k_norm, apply_rotary_emb_k, store_kvcache).
+ * Per token t and head h (head_dim D = 128, neox halves x1 = x[:64], x2 = x[64:]):
+ *   RMSNorm (when the head's weight is non-NULL): y = dtype(float(x) / sqrt(mean(float(x)^2) + eps)), then
+ *   y = dtype(float(y) * float(weight)); rotary: with c = cos_sin_cache[p, :64], s = cos_sin_cache[p, 64:] and
+ *   p = positions[t] (clamped into [0, cache_positions)), o = dtype(concat(y1*c - y2*s, y2*c + y1*s)), every
+ *   product and sum rounded separately as in the eager ops.
+ * q_out[t, h] = o for query heads (q_out may alias q); for key heads o goes to k_out (when non-NULL) and, like v, to
+ * cache slot slot_mapping[t] (skipped when negative or >= cache_slots, as store_kvcache skips -1).
+ * q, k, v, q_out, k_out: [n_tokens, heads, 128] with the given token strides and head stride 128 (views of the fused
+ * qkv output are fine); weights [128] in the same dtype; cos_sin_cache [cache_positions, 128] fp32 (the
+ * reference's cos_sin_cache buffer); caches [cache_slots, n_kv_heads, 128]. dtype bf16 or fp16. */
+int nvs_qk_norm_rope_store(const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride,
+                           const void* v, int64_t v_token_stride, const int64_t* positions,
+                           const void* q_norm_weight, const void* k_norm_weight, float eps,
+                           const float* cos_sin_cache, int64_t cache_positions,
+                           const int32_t* slot_mapping, void* k_cache, void* v_cache, int64_t cache_slots,
+                           void* q_out, int64_t q_out_token_stride, void* k_out, int64_t k_out_token_stride,
+                           int64_t n_tokens, int n_heads, int n_kv_heads, int head_dim, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------------------------------ attention
  * Replaces both flash-attn calls of Attention.forward (nanovllm/layers/attention.py:59-77):

@@ -72,6 +72,28 @@ __device__ __forceinline__ float load_as_float(const void* base, int64_t idx) {
     }
 }
 
+// Wave reductions through DPP (no LDS round trips): rotations by 8, 4, 2 and 1 inside each 16-lane row leave
+// every lane with its row's result; row_bcast:15 folds row 0 into row 1 and row 2 into row 3, row_bcast:31 folds
+// rows 0-1 into rows 2-3, so lane 63 holds the wave's result, which readlane hands to every lane. Lanes of rows
+// a broadcast does not write get `old`: the identity for a sum, the lane's own value for a max. The whole wave
+// must be active.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t src) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(src), CTRL, ROWS, 0xf, false));
+}
+
+// fp32 sum over the wave in a fixed order (the same result on every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+    v += __uint_as_float(dpp_u32<0x128, 0xf>(0u, __float_as_uint(v)));   // row_ror:8
+    v += __uint_as_float(dpp_u32<0x124, 0xf>(0u, __float_as_uint(v)));   // row_ror:4
+    v += __uint_as_float(dpp_u32<0x122, 0xf>(0u, __float_as_uint(v)));   // row_ror:2
+    v += __uint_as_float(dpp_u32<0x121, 0xf>(0u, __float_as_uint(v)));   // row_ror:1
+    v += __uint_as_float(dpp_u32<0x142, 0xa>(0u, __float_as_uint(v)));   // row_bcast:15
+    v += __uint_as_float(dpp_u32<0x143, 0xc>(0u, __float_as_uint(v)));   // row_bcast:31
+    return __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(v)), 63)));
+}
+
 // Order-preserving map of fp32 onto uint32: a < b  <=>  key(a) < key(b) (for non-NaN; -0 < +0).
 __device__ __forceinline__ uint32_t float_key(float f) {
     uint32_t u = __float_as_uint(f);

@@ -111,26 +111,9 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 // already executes them in order).
 __device__ __forceinline__ void compiler_fence_s() { asm volatile("" ::: "memory"); }
 
-// Wave reductions through DPP (no LDS round trips): rotations by 8, 4, 2 and 1 inside each 16-lane row leave
-// every lane with its row's result; row_bcast:15 folds row 0 into row 1 and row 2 into row 3, row_bcast:31 folds
-// rows 0-1 into rows 2-3, so lane 63 holds the wave's result, which readlane hands to every lane. Lanes of rows
-// a broadcast does not write get `old`: the identity for a sum, the lane's own value for a max.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t src) {
-    return static_cast<uint32_t>(
-        __builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(src), CTRL, ROWS, 0xf, false));
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-    auto step = [](float x, float y) { return x + y; };
-    v = step(v, __uint_as_float(dpp_u32<0x128, 0xf>(0u, __float_as_uint(v))));   // row_ror:8
-    v = step(v, __uint_as_float(dpp_u32<0x124, 0xf>(0u, __float_as_uint(v))));   // row_ror:4
-    v = step(v, __uint_as_float(dpp_u32<0x122, 0xf>(0u, __float_as_uint(v))));   // row_ror:2
-    v = step(v, __uint_as_float(dpp_u32<0x121, 0xf>(0u, __float_as_uint(v))));   // row_ror:1
-    v = step(v, __uint_as_float(dpp_u32<0x142, 0xa>(0u, __float_as_uint(v))));   // row_bcast:15
-    v = step(v, __uint_as_float(dpp_u32<0x143, 0xc>(0u, __float_as_uint(v))));   // row_bcast:31
-    return __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(v)), 63)));
-}
+// Wave reductions through DPP (nvs::dpp_u32): the max forms use the lane's own value as `old`.
+using nvs::dpp_u32;
+using nvs::wave_sum;
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     v = max(v, dpp_u32<0x128, 0xf>(v, v));

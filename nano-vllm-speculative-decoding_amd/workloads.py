@@ -206,3 +206,67 @@ def sampler_case(batch: int, num_drafts: int, vocab: int, top_k: int | list[int]
                        verified_lens=lens, temperatures=temps, top_k=tk, top_p=tp,
                        max_top_k=int(tk.max()), has_top_p=bool((tp < 1.0).any()), uniforms=uniforms, noise=noise)
     return case.to(device) if device != "cpu" else case
+
+
+@dataclass
+class QkRopeCase:
+    """Inputs of the q/k norm + rotary + KV store step of one layer: the fused qkv projection output
+    [T, (Hq + 2 Hkv) * D] (q, k, v are views of it, as qwen3.py:79-81 splits it), token positions, the q/k norm
+    weights, the rotary table, and a paged cache with the slots of the tokens (-1 for padding tokens)."""
+    qkv: torch.Tensor             # [T, (Hq + 2 Hkv) * D]
+    positions: torch.Tensor       # [T] int64
+    q_norm_weight: torch.Tensor   # [D]
+    k_norm_weight: torch.Tensor   # [D]
+    table: torch.Tensor           # [P, D] fp32 cos | sin
+    slot_mapping: torch.Tensor    # [T] int32
+    k_cache: torch.Tensor         # [blocks, bs, Hkv, D]
+    v_cache: torch.Tensor
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    eps: float = 1e-6
+
+    def split(self):
+        """(q, k, v) views [T, H, D] of the fused projection output."""
+        hq, hkv, d = self.num_heads, self.num_kv_heads, self.head_dim
+        q, k, v = self.qkv.split([hq * d, hkv * d, hkv * d], dim=-1)
+        return q.view(-1, hq, d), k.view(-1, hkv, d), v.view(-1, hkv, d)
+
+    def to(self, device) -> "QkRopeCase":
+        fields = {name: getattr(self, name) for name in self.__dataclass_fields__}
+        for name, value in fields.items():
+            if isinstance(value, torch.Tensor):
+                fields[name] = value.to(device)
+        return QkRopeCase(**fields)
+
+    def bytes_moved(self) -> int:
+        """HBM bytes of the fused step: read q, k, v, positions, slots, the table rows and the weights; write the
+        rotated q and the K/V rows of every stored token."""
+        T = self.qkv.shape[0]
+        es = self.qkv.element_size()
+        d, hq, hkv = self.head_dim, self.num_heads, self.num_kv_heads
+        stored = int((self.slot_mapping >= 0).sum())
+        return (T * (hq + 2 * hkv) * d * es + T * (8 + 4) + T * d * 4 + 2 * d * es
+                + T * hq * d * es + stored * 2 * hkv * d * es)
+
+
+def qk_rope_case(num_tokens: int, num_heads: int = 32, num_kv_heads: int = 8, head_dim: int = 128,
+                 num_padding: int = 8, max_position: int = 40960, rope_theta: float = 1e6, block_size: int = 256,
+                 dtype=torch.bfloat16, seed: int = 0) -> QkRopeCase:
+    """Qwen3-8B-shaped by default (rope_theta 1e6, 40,960 positions). The last num_padding tokens carry slot -1; the
+    others go to distinct random slots of a cache with room for all of them."""
+    from .layers.qk_norm_rope import rope_cos_sin_cache
+    g = torch.Generator().manual_seed(seed)
+    width = (num_heads + 2 * num_kv_heads) * head_dim
+    qkv = (torch.randn(num_tokens, width, generator=g) * 2).to(dtype)
+    positions = torch.randint(0, max_position, (num_tokens,), generator=g)
+    q_w = (1 + 0.1 * torch.randn(head_dim, generator=g)).to(dtype)
+    k_w = (1 + 0.1 * torch.randn(head_dim, generator=g)).to(dtype)
+    table = rope_cos_sin_cache(head_dim, max_position, rope_theta, torch.device("cpu"))
+    blocks = (num_tokens + block_size - 1) // block_size + 1
+    slots = torch.randperm(blocks * block_size, generator=g)[:num_tokens].to(torch.int32)
+    if num_padding:
+        slots[-num_padding:] = -1
+    k_cache = torch.zeros(blocks, block_size, num_kv_heads, head_dim, dtype=dtype)
+    return QkRopeCase(qkv, positions, q_w, k_w, table, slots, k_cache, torch.zeros_like(k_cache), num_heads,
+                      num_kv_heads, head_dim)

@@ -8,6 +8,7 @@ Modules
   oracle.attention     paged KV store and paged multi-query attention: an fp64 numpy brute force and a torch fp32
                        restatement of the reference's CPU stand-in (tests/fake_paged_attention.py)
   oracle.spec_sampler  torch-CPU restatement of nanovllm/layers/spec_sampler.py, with the random draws passed in
+  oracle.qk_norm_rope  eager q/k RMSNorm + rotary embedding + KV store (layernorm.py, rotary_embedding.py, qwen3.py)
 
 How each function is pinned (each check fails for a dropped term, a wrong sign or index, a transposed operand):
   attention.store_kvcache       exact-copy semantics, a known slot layout (tests/test_oracle_attention.py)
@@ -15,6 +16,9 @@ How each function is pinned (each check fails for a dropped term, a wrong sign o
                                 scale 0 -> mean), a dense-attention brute force with an explicit mask, GQA head
                                 mapping by construction, block-table permutation invariance
   attention.paged_attention_t32 agreement with the fp64 brute force (fp32 tolerance)
+  qk_norm_rope.*                RMSNorm closed forms and fp64, the rotary table against its frequency formula, the
+                                rotation against the fp64 complex product (identity at 0, composition, norms,
+                                relative-position scores), a planted interleaved rotation that must differ
   spec_sampler.*                every known answer of the reference's tests/test_spec_sampler.py, the
                                 fixed-length body the variable-length rewrite must reproduce bit for bit, exact
                                 Fraction enumeration of the frozen cases (SHA-256 pinned), Hoeffding-bound

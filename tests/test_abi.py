@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version_and_empty_error(lib):
-    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 2
     assert isinstance(lib.nvs_last_error(), bytes)
 
 
@@ -108,3 +108,19 @@ def test_store_kvcache_rejects_bad_arguments(lib):
     assert lib.nvs_store_kvcache(1 << 20, 512, 1 << 20, 1024, 1 << 21, 1 << 22, 100, 1 << 23, 4, 8, 128,
                                  _lib.DTYPE_BF16, None) == _lib.NVS_ERR_INVALID
     assert lib.nvs_store_kvcache(None, 0, None, 0, None, None, 0, None, 0, 8, 128, _lib.DTYPE_BF16, None) == 0
+
+
+def test_qk_norm_rope_store_rejects_bad_arguments(lib):
+    def call(**over):
+        a = dict(q=1 << 20, q_ts=6144, k=1 << 21, k_ts=6144, v=1 << 22, v_ts=6144, pos=1 << 23, qw=None, kw=None,
+                 eps=1e-6, cs=1 << 24, n_cs=4096, slots=None, kc=None, vc=None, cache_slots=0, qo=1 << 25,
+                 qo_ts=4096, ko=None, ko_ts=0, T=4, hq=32, hkv=8, d=128, dtype=_lib.DTYPE_BF16, stream=None)
+        a.update(over)
+        return lib.nvs_qk_norm_rope_store(*a.values())
+    assert call(dtype=_lib.DTYPE_F32) == _lib.NVS_ERR_UNSUPPORTED
+    assert call(d=64) == _lib.NVS_ERR_UNSUPPORTED
+    assert call(q=None) == _lib.NVS_ERR_INVALID            # query heads without q
+    assert call(k_ts=512) == _lib.NVS_ERR_INVALID          # shorter than 8 heads x 128
+    assert call(slots=1 << 26) == _lib.NVS_ERR_INVALID     # slots without caches
+    assert call(n_cs=0) == _lib.NVS_ERR_INVALID
+    assert call(T=0) == _lib.NVS_OK                        # nothing to do, nothing launched
