@@ -140,11 +140,61 @@ def sampler_bench(args, dev):
     torch.cuda.synchronize()
     del step_out
     log(f"[bench] fused sampler: {ms * 1e3:.1f} us, {gbs:.0f} GB/s = {100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
-    return {"workload": "spec_accept_b64_k7_v151936_fp32_topk64", "us": round(ms * 1e3, 2),
+
+    # the production dtype of the target logits (bf16: half the bytes) and the greedy accept over the same rows
+    lg16 = g.logits.to(torch.bfloat16)
+
+    def step16():
+        ns.spec_accept_with_draws(lg16, g.q, g.drafts, st, None, g.uniforms, g.noise, workspace=ws)
+
+    ms16 = time_gpu(step16, max(10, args.steps // 2), max(3, args.warmup // 2))
+    lg3 = g.logits.view(64, 8, V)
+
+    def greedy():
+        ns.accept_greedy(lg3, g.drafts)
+
+    msg = time_gpu(greedy, max(10, args.steps // 2), max(3, args.warmup // 2))
+    log(f"[bench] fused sampler on bf16 logits: {ms16 * 1e3:.1f} us; greedy accept (fp32): {msg * 1e3:.1f} us")
+    variants = {
+        "bf16_logits": {"us": round(ms16 * 1e3, 2), "GBs": round(alg / 2 / (ms16 * 1e-3) / 1e9, 1),
+                        "algorithmic_bytes": alg // 2},
+        "greedy_fp32": {"us": round(msg * 1e3, 2), "GBs": round(alg / (msg * 1e-3) / 1e9, 1),
+                        "algorithmic_bytes": alg, "kernel": "argmax_kernel + greedy_finalize_kernel"},
+    }
+    return {"workload": "spec_accept_b64_k7_v151936_fp32_topk64", "us": round(ms * 1e3, 2), "variants": variants,
             "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": alg,
             "traffic": MEASURED_TRAFFIC["spec_accept_b64_k7_v151936_fp32_topk64"],
             "kernel": "select_kernel<f32, accept> (one launch per call)",
             "mean_accepted": round(float(n.float().mean()), 3)}
+
+
+def draft_block_bench(args, dev):
+    """The draft model's block attention (the decode branch run by DFlashDrafter, speculative.py:268-275): 64 rows
+    of 7 block queries each, non-causal over their whole context (2,807-3,207 keys, the same 3k contexts as the
+    verify layer plus the block), Qwen3-8B-shaped heads, fixed-length mode."""
+    import torch
+
+    import nvs_amd.workloads as wl
+    from nvs_amd.layers import attention as nattn
+    lq = 7
+    _, k_lens = wl.random_lengths(64, (1, 8), (2800 + lq, 3200 + lq), seed=1)
+    case = wl.verify_attention_case([lq] * 64, k_lens, 32, 8, 128, pad_tokens_to=1)
+    g = case.to(dev)
+    ctx = torch.tensor(k_lens, dtype=torch.int32, device=dev)
+    out = torch.empty_like(g.q)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+
+    def step():
+        nattn._paged_attention(g.q, g.k_cache, g.v_cache, g.block_tables, None, None, ctx, lq, 64, lq, 4096,
+                               g.scale, False, out=out, workspace=ws)
+
+    ms = time_gpu(step, args.steps, args.warmup)
+    b = case.kv_bytes() + case.qo_bytes()
+    gbs = b / (ms * 1e-3) / 1e9
+    log(f"[bench] draft-block attention (Lq 7, non-causal): {ms * 1e3:.1f} us, {gbs:.0f} GB/s = "
+        f"{100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
+    return {"workload": "draft_block_attention_qwen3_8b_b64_lq7_noncausal_ctx2807_3207", "us": round(ms * 1e3, 2),
+            "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": b}
 
 
 def qk_rope_bench(args, dev):
@@ -272,7 +322,8 @@ def main():
     dev = torch.device("cuda", 0)
 
     case, ms, nbytes, gbs, flops = attention_bench(args, dev)
-    extra = {"c2": launch_bound_bench(args, dev), "qk_norm_rope_store": qk_rope_bench(args, dev)}
+    extra = {"c2": launch_bound_bench(args, dev), "draft_block": draft_block_bench(args, dev),
+             "qk_norm_rope_store": qk_rope_bench(args, dev)}
     if args.sampler == "on":
         extra["sampler"] = sampler_bench(args, dev)
     if args.copy_probe == "on":
