@@ -154,8 +154,18 @@ def sampler_bench(args, dev):
         ns.accept_greedy(lg3, g.drafts)
 
     msg = time_gpu(greedy, max(10, args.steps // 2), max(3, args.warmup // 2))
-    log(f"[bench] fused sampler on bf16 logits: {ms16 * 1e3:.1f} us; greedy accept (fp32): {msg * 1e3:.1f} us")
+    # top-p 0.9 and temperature 0.7 on every row (the nucleus path and the IEEE division by the temperature)
+    st_p = ns.SamplingTensors(torch.full_like(g.temperatures, 0.7), g.top_k, torch.full_like(g.top_p, 0.9),
+                              case.max_top_k, True, True)
+
+    def step_p():
+        ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st_p, None, g.uniforms, g.noise, workspace=ws)
+
+    msp = time_gpu(step_p, max(10, args.steps // 2), max(3, args.warmup // 2))
+    log(f"[bench] fused sampler on bf16 logits: {ms16 * 1e3:.1f} us; top-p 0.9 + temperature 0.7: "
+        f"{msp * 1e3:.1f} us; greedy accept (fp32): {msg * 1e3:.1f} us")
     variants = {
+        "topp0.9_temp0.7": {"us": round(msp * 1e3, 2), "GBs": round(alg / (msp * 1e-3) / 1e9, 1)},
         "bf16_logits": {"us": round(ms16 * 1e3, 2), "GBs": round(alg / 2 / (ms16 * 1e-3) / 1e9, 1),
                         "algorithmic_bytes": alg // 2},
         "greedy_fp32": {"us": round(msg * 1e3, 2), "GBs": round(alg / (msg * 1e-3) / 1e9, 1),

@@ -845,6 +845,15 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         int lcnt = 0;           // this lane's list length
         uint32_t hmax = 0u;     // largest key this lane appended
         bool overflow = false;  // the same on every lane of the wave
+        // With a positive temperature the pass compares raw values: x / t rounds monotonically in x, so the K-th
+        // largest scaled value is the K-th largest raw value divided by t, and the lists are scaled once at the end
+        // of the pass instead of every value in it. Two adjacent raw values can divide to the same quotient, so the
+        // raw bound is lowered by one unit in the last place: a value just below it whose quotient ties with the
+        // bound's is listed too. A temperature that is not positive and finite scales every value in the pass.
+        const bool raw_mode = !unit_temp && temp > 0.f && temp < INFINITY;
+        const bool scale_in_pass = !unit_temp && !raw_mode;
+        const uint32_t slack = raw_mode ? 1u : 0u;
+        auto key_bound = [&](uint32_t k) { return k <= slack ? -INFINITY : nvs::key_float(k - slack); };
 
         // A tighter bound from this wave's lists: one 256-bin histogram of the listed keys at or above tau, the
         // bins spread over [tau, the wave's largest key]; the lower edge of the bin holding the wave's K-th largest
@@ -873,7 +882,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                 if (b < 256u && b > 0u) {
                     const uint32_t kb = tau_key + (b << sh_bits);
                     tau_key = kb;
-                    tau = nvs::key_float(kb);
+                    tau = key_bound(kb);
                     atomicMax(&sh.tau_key, kb);
                 }
             }
@@ -895,9 +904,9 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
 
         // Filter one batch. Most batches hold no element at or above tau in the whole wave: one max, one compare,
         // one ballot. Otherwise each lane with a passing value appends it to its own list.
-        auto filter = [&](float (&sv)[kVpt], int bi) {   // scales the buffer in place (it is reloaded next)
+        auto filter = [&](float (&sv)[kVpt], int bi) {   // may scale the buffer in place (it is reloaded next)
             const int64_t e0 = static_cast<int64_t>(bi) * kBatch;
-            if (!unit_temp) {
+            if (scale_in_pass) {
 #pragma unroll
                 for (int vi = 0; vi < kVpt; ++vi) sv[vi] = sv[vi] / temp;
             }
@@ -913,7 +922,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             if (overflow || __ballot(hi >= tau) == 0ull) return;
             if (shared_key > tau_key) {   // another wave raised the bound
                 tau_key = shared_key;
-                tau = nvs::key_float(shared_key);
+                tau = key_bound(shared_key);
             }
             if (hi >= tau) {
 #pragma unroll
@@ -961,7 +970,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                 mn = fminf(mn, fminf(ina ? ra[vi] : INFINITY, inb ? rb[vi] : INFINITY));
             }
             // A lane with nothing (or only -inf) counts as holding nothing: that can only lower the bound.
-            const float ext = scale_logit(temp < 0.f ? mn : mx, temp, unit_temp);
+            const float ext = scale_in_pass ? scale_logit(temp < 0.f ? mn : mx, temp, unit_temp) : mx;
             const uint32_t tmax = (ext == -INFINITY || ext != ext) ? 0u : sel_key(ext);
             const int rw = (K + kSelWaves - 1) / kSelWaves;
             uint32_t bound = 0u;
@@ -974,7 +983,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             uint32_t b = 0xffffffffu;
             for (int w = 0; w < kSelWaves; ++w) b = min(b, sh.ured[w]);
             tau_key = b;
-            tau = (b == 0u) ? -INFINITY : nvs::key_float(b);   // NaN never passes a >= test
+            tau = key_bound(b);   // -inf for no bound; NaN never passes a >= test
         }
         if constexpr (VEC) {
             // each buffer is reloaded with the batch three ahead as soon as it is filtered
@@ -1001,6 +1010,13 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             }
         }
         lcnt = min(lcnt, kLaneCap);   // past it only when the row goes to the exact path
+        if (raw_mode) {
+            // the lists, the bound and the largest key move to scaled values: one division per listed value
+            for (int s = 0; s < lcnt; ++s)
+                wkey[s * 64 + lane] = nvs::float_key(nvs::key_float(wkey[s * 64 + lane]) / temp);
+            tau_key = tau_key == 0u ? 0u : nvs::float_key(nvs::key_float(tau_key) / temp);
+            hmax = hmax == 0u ? 0u : nvs::float_key(nvs::key_float(hmax) / temp);
+        }
         const uint32_t wave_hi = wave_max_u32(hmax);
         const int wave_total = wave_sum_i32(lcnt);
         const int max_cnt = static_cast<int>(wave_max_u32(static_cast<uint32_t>(lcnt)));
