@@ -139,9 +139,9 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     v = dpp_max_u64<0x121, 0xf>(v);
     v = dpp_max_u64<0x142, 0xa>(v);
     v = dpp_max_u64<0x143, 0xc>(v);
-    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), 63));
-    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), 63));
-    return (static_cast<uint64_t>(hi) << 32) | lo;
+    const int lo = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), 63);
+    const int hi = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), 63);
+    return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
 }
 
 // Inclusive prefix sum over the wave.
@@ -579,6 +579,25 @@ __device__ float top_p_threshold(SelShared& sh, int rank, int K, float top_p, fl
     }
     __syncthreads();
     return result;
+}
+
+// The same threshold computed by one wave when rank <= 64: lane l holds the l-th largest candidate key (the
+// rank-th largest repeated where candidates tie with it, as top-k ranks beyond it are -inf), 0 past rank. Every
+// lane gets the result.
+__device__ float wave_top_p_threshold64(uint32_t key_l, int rank, int K, float top_p, float thr) {
+    const int l = lane_id();
+    const float m = nvs::key_float(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(key_l))));
+    const float e = (l < rank) ? expf(nvs::key_float(key_l) - m) : 0.f;
+    const float total = wave_sum(e);
+    const float nucleus = e / total;
+    const float cum = wave_scan_incl(nucleus);
+    const float before = cum - nucleus;
+    int kept_all = __popcll(__ballot(l < rank && before < top_p));
+    const float last_cum = __shfl(cum, 63);   // cumsum at rank - 1 (all later entries add zero)
+    if (last_cum < top_p) kept_all += K - rank;
+    const uint32_t at = static_cast<uint32_t>(__shfl(static_cast<int>(key_l), max(kept_all - 1, 0)));
+    const float p_thr = (kept_all >= 1 && kept_all - 1 < rank) ? nvs::key_float(at) : -INFINITY;
+    return fmaxf(thr, p_thr);
 }
 
 struct RowStats {
@@ -1037,14 +1056,14 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         // fewer listed keys than the rank (NaN logits never join a list): the exact path decides the row
         bool exact = sh.overflow || listed < rank;
 
-        // Without top-p: every key at or above lo (the largest of the waves' bounds, still at most the K-th
-        // largest, and every such key is listed) goes into one 256-bin histogram over [lo, hi], the bins spread
-        // over that range so few keys share one. The bin holding the rank-th largest and the bins above it hold
-        // few keys; they move to one short list (the bin's own keys also to a second), where wave 0 finds the
-        // threshold by counting and finishes the row.
+        // Fast path (no top-p, or top-p with rank <= 64): every key at or above lo (the largest of the waves'
+        // bounds, still at most the K-th largest, and every such key is listed) goes into one 256-bin histogram
+        // over [lo, hi], the bins spread over that range so few keys share one. The bin holding the rank-th largest
+        // and the bins above it hold few keys; they move to one short list (the bin's own keys also to a second),
+        // where wave 0 finds the threshold by counting, applies top-p, and finishes the row.
         constexpr int kTopCap = kSelWaves * 64;   // short-list capacity: indices follow the keys in sortbuf
         uint32_t* bin_keys = &sh.whist[0][0];
-        bool fast = !exact && !a.has_top_p;
+        bool fast = !exact && (!a.has_top_p || rank <= 64);
         uint32_t lo = 0u, hi = 0u, bin = 0u, bin_rank = 0u;
         int shift = 0;
         if (fast) {
@@ -1114,19 +1133,44 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                 const int n_top = sh.count;
                 uint32_t kk[kSelWaves];
                 int32_t ki[kSelWaves];
-                float z = 0.f;
 #pragma unroll
                 for (int w = 0; w < kSelWaves; ++w) {
                     const int c = w * 64 + lane;
                     kk[w] = c < n_top ? sh.sortbuf[c] : 0u;
                     ki[w] = c < n_top ? static_cast<int32_t>(sh.sortbuf[kTopCap + c]) : 0;
-                    if (kk[w] >= thr_key) z += expf(nvs::key_float(kk[w]) - mu_f);
                 }
+                uint32_t theta_key = thr_key;
+                if (a.has_top_p) {
+                    // top-p over the rank candidates (rank <= 64): the keys above the threshold (fewer than rank)
+                    // sorted into lanes, the threshold repeated up to rank (truncate_logits' -inf beyond it)
+                    uint32_t* gbuf = sh.hist;   // free once the short list is formed
+                    int g = 0;
+#pragma unroll
+                    for (int w = 0; w < kSelWaves; ++w) {
+                        const bool gt = kk[w] > thr_key;
+                        const uint64_t bal = __ballot(gt);
+                        if (gt)
+                            gbuf[g + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                          static_cast<uint32_t>(bal >> 32),
+                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)))] = kk[w];
+                        g += __popcll(bal);
+                    }
+                    compiler_fence_s();
+                    const uint32_t sorted = wave_sort_desc(lane < g ? gbuf[lane] : 0u);
+                    const uint32_t key_l = lane < g ? sorted : (lane < rank ? thr_key : 0u);
+                    const float theta =
+                        wave_top_p_threshold64(key_l, rank, K, top_p, nvs::key_float(thr_key));
+                    theta_key = (theta == -INFINITY) ? thr_key : nvs::float_key(theta);
+                }
+                float z = 0.f;
+#pragma unroll
+                for (int w = 0; w < kSelWaves; ++w)
+                    if (kk[w] >= theta_key) z += expf(nvs::key_float(kk[w]) - mu_f);
                 z = wave_sum(z);
                 if (lane == 0) {
                     sh.fast_m = m;
                     sh.fast_z = z;
-                    sh.fast_theta = nvs::key_float(thr_key);
+                    sh.fast_theta = nvs::key_float(theta_key);
                 }
                 if constexpr (MODE == kModeAccept) {
                     const int64_t b = sh.loc[0], j = sh.loc[1], L = sh.loc[2];
@@ -1135,7 +1179,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                     int acc = 0;
                     if (lane == 0 && dec_valid) {
                         const float sd = scale_logit(dec_x, temp, unit_temp);
-                        const float pd = (sel_key(sd) >= thr_key && sel_key(sd) != 0u) ? expf(sd - mu_f) / z : 0.f;
+                        const float pd = (sel_key(sd) >= theta_key && sel_key(sd) != 0u) ? expf(sd - mu_f) / z : 0.f;
                         acc = (dec_u * dec_q < pd) ? 1 : 0;
                     }
                     const float* qrow = a.q + (b * kd + (bonus ? 0 : j)) * a.vocab;
@@ -1144,14 +1188,14 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                     float qv[kSelWaves], ev[kSelWaves];
 #pragma unroll
                     for (int w = 0; w < kSelWaves; ++w) {
-                        const int64_t ix = kk[w] >= thr_key ? static_cast<int64_t>(ki[w]) : int64_t{0};
+                        const int64_t ix = kk[w] >= theta_key ? static_cast<int64_t>(ki[w]) : int64_t{0};
                         qv[w] = bonus ? 0.f : qrow[ix];
                         ev[w] = erow[ix];
                     }
                     uint64_t best = 0;
 #pragma unroll
                     for (int w = 0; w < kSelWaves; ++w) {
-                        if (kk[w] < thr_key) continue;
+                        if (kk[w] < theta_key) continue;
                         const float p = expf(nvs::key_float(kk[w]) - mu_f) / z;
                         const float wgt = bonus ? p : fmaxf(p - qv[w], 0.f);
                         const float score = wgt / ev[w];
@@ -1164,7 +1208,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                         PosRecord r;
                         r.m = m;
                         r.z = z;
-                        r.theta = nvs::key_float(thr_key);
+                        r.theta = nvs::key_float(theta_key);
                         r.temp = temp;
                         r.flags = 0;
                         r.acc = acc;
