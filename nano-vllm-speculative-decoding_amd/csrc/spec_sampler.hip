@@ -266,14 +266,9 @@ __device__ void radix_pick_digit(SelShared& sh) {
             h[i] = sh.hist[4 * l + i];
             tot += h[i];
         }
-        // exclusive suffix sum over lanes: counts in bins of higher lanes
-        uint32_t suf = tot;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t w = static_cast<uint32_t>(__shfl_down(static_cast<int>(suf), o));
-            if (l + o < 64) suf += w;
-        }
-        uint32_t above = suf - tot;  // keys in bins of lanes > l
+        // exclusive suffix sum over lanes (counts in bins of higher lanes) = total - inclusive prefix
+        const int incl = wave_scan_incl_dpp(static_cast<int>(tot));
+        uint32_t above = static_cast<uint32_t>(__builtin_amdgcn_readlane(incl, 63) - incl);  // bins of lanes > l
         const uint32_t rem = sh.sel_remaining;
 #pragma unroll
         for (int i = 3; i >= 0; --i) {
@@ -463,13 +458,9 @@ __device__ __forceinline__ void wave_pick_bin(const uint32_t* hist, uint32_t ran
         h[i] = hist[4 * l + i];
         tot += h[i];
     }
-    uint32_t suf = tot;  // inclusive suffix sum over lanes
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t w = static_cast<uint32_t>(__shfl_down(static_cast<int>(suf), o));
-        if (l + o < 64) suf += w;
-    }
-    uint32_t above = suf - tot;
+    // keys in bins of lanes > l: the total minus the inclusive prefix
+    const int incl = wave_scan_incl_dpp(static_cast<int>(tot));
+    uint32_t above = static_cast<uint32_t>(__builtin_amdgcn_readlane(incl, 63) - incl);
     int found_bin = -1;
     uint32_t found_rem = 0;
 #pragma unroll
@@ -992,10 +983,15 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             const float ext = scale_in_pass ? scale_logit(temp < 0.f ? mn : mx, temp, unit_temp) : mx;
             const uint32_t tmax = (ext == -INFINITY || ext != ext) ? 0u : sel_key(ext);
             const int rw = (K + kSelWaves - 1) / kSelWaves;
+            // the rw-th largest lane maximum, bit by bit from the top: the largest key with at least rw lanes at or
+            // above it (one compare and one ballot per bit, no cross-lane data movement)
             uint32_t bound = 0u;
             if (rw <= 64) {
-                const uint32_t sorted = wave_sort_desc(tmax);
-                bound = static_cast<uint32_t>(__shfl(static_cast<int>(sorted), rw - 1));
+#pragma unroll
+                for (int bit = 31; bit >= 0; --bit) {
+                    const uint32_t cand = bound | (1u << bit);
+                    if (__popcll(__ballot(tmax >= cand)) >= rw) bound = cand;
+                }
             }
             if (lane == 0) sh.ured[wave] = bound;
             __syncthreads();
