@@ -10,8 +10,11 @@ Also measured: the fused speculative sampler (64 rows x 8 verified positions, V 
 top-k 64), against the one read of the [512, V] logits it must make; and the torch-CPU restatement of the same
 attention (the oracle, the reference's CPU path) on the host cores as a reported baseline.
 
+Also: a whole verify round of 36 Qwen3-8B-shaped layers (random bf16 weights) captured as a HIP graph, with the
+logits and the fused accept, against its HBM floor (weights + K/V + logits).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-baseline on|off] [--sampler on|off]
-                       [--copy-probe on|off]
+                       [--verify-round on|off] [--copy-probe on|off]
 """
 import argparse
 import json
@@ -270,6 +273,73 @@ def qk_rope_bench(args, dev):
             "timing": "HIP graph of 20 calls, per call", "kernel": "qk_norm_rope_store_kernel (one launch)"}
 
 
+def verify_round_bench(args, dev):
+    """A whole verify round (the round-level workload): 36 Qwen3-8B-shaped layers over the batch-64 verify batch
+    (the attention workload's rows, one forward captured as a HIP graph on the reference's (row slots, tokens)
+    shape), the bf16 logits of the verified tokens, and the fused accept (top-k 64, temperature 1) on them.
+    Floor: the weights (15.14 GB) + 36 layers of K/V + the logits written once and read once, at 8 TB/s."""
+    import torch
+
+    from nvs_amd import verify_round as vr
+    from nvs_amd.layers import spec_sampler as ns
+
+    log("[bench] building the 36-layer Qwen3-8B verify round (random bf16 weights, paged KV per layer)")
+    shape = vr.QWEN3_8B
+    batch = vr.random_verify_batch(64)
+    target = vr.Qwen3VerifyTarget(shape, batch.num_blocks, device=dev)
+    graphs = vr.VerifyGraphs(target, max_batch_size=512, query_len=8, max_model_len=4096)
+    rows, tokens = graphs.shape_for(batch.num_tokens)
+    graphs.capture([tokens])
+    B, k, V, T = len(batch.q_lens), 7, shape.vocab_size, batch.num_tokens
+    g = torch.Generator(device=dev).manual_seed(11)
+    ids = torch.randint(0, V, (T,), device=dev, generator=g)
+    # the drafter's output: a top-64 softmax of N(0, 9) draft logits, drafts drawn from it
+    q = torch.randn(B, k, V, device=dev, generator=g).mul_(3.0)
+    kth = q.topk(64, dim=-1).values[..., -1:]
+    q = torch.softmax(q.masked_fill_(q < kth, float("-inf")), dim=-1)
+    drafts = (q / torch.empty_like(q).exponential_(generator=g)).argmax(-1)
+    lens = torch.tensor(batch.q_lens, dtype=torch.int64, device=dev)
+    st = ns.SamplingTensors(torch.ones(B, device=dev), torch.full((B,), 64, dtype=torch.int64, device=dev),
+                            torch.ones(B, device=dev), 64, False, True)
+    gen = torch.Generator(device=dev).manual_seed(12)
+    hidden = graphs.run(batch, ids)
+
+    def whole():
+        h = graphs.run(batch, ids)
+        return ns.accept_from_logits(target.compute_logits(h), q, drafts, st, lens, gen)
+
+    def forward_only():
+        graphs.graphs[tokens].replay()
+
+    def tail_only():
+        ns.accept_from_logits(target.compute_logits(hidden), q, drafts, st, lens, gen)
+
+    def greedy_round():   # temperature 0: the argmax accept on the same logits (spec_sampler.py:161-169)
+        h = graphs.run(batch, ids)
+        return ns.accept_greedy_varlen(target.compute_logits(h), drafts, lens)
+
+    steps, warm = max(5, args.steps // 10), max(2, args.warmup // 5)
+    ms = time_gpu(whole, steps, warm)
+    ms_fwd = time_gpu(forward_only, steps, warm)
+    ms_tail = time_gpu(tail_only, steps, warm)
+    ms_greedy = time_gpu(greedy_round, steps, warm)
+    n_accept, _ = whole()
+    weights = shape.streamed_weight_bytes()
+    kv = shape.num_layers * batch.kv_bytes(shape.num_kv_heads, shape.head_dim)
+    logits = 2 * T * V * 2
+    floor_ms = (weights + kv + logits) / (HBM_PEAK_GBS * 1e9) * 1e3
+    log(f"[bench] verify round: {ms:.3f} ms (forward graph {ms_fwd:.3f} ms, logits + accept {ms_tail:.3f} ms); "
+        f"HBM floor {floor_ms:.3f} ms = {100 * floor_ms / ms:.1f}% of the floor's speed; greedy round {ms_greedy:.3f} ms")
+    return {"workload": "verify_round_qwen3_8b_36_layers_b64_varlen_q1_8_ctx2800_3200_topk64",
+            "ms_per_round": round(ms, 4), "forward_graph_ms": round(ms_fwd, 4),
+            "logits_and_accept_ms": round(ms_tail, 4), "greedy_round_ms": round(ms_greedy, 4),
+            "floor_ms": round(floor_ms, 4),
+            "frac_of_floor": round(floor_ms / ms, 4),
+            "floor_bytes": {"weights": weights, "kv": kv, "logits_write_and_read": logits},
+            "graph_shape": {"row_slots": rows, "tokens": tokens, "verified_tokens": T},
+            "mean_accepted": round(float(n_accept.float().mean()), 3)}
+
+
 def copy_probe(args, dev):
     """A plain 1 GiB device-to-device copy: the HBM rate a streaming kernel can reach on this box, and, under
     rocprofv3 --pmc, the known-size kernel that scales FETCH_SIZE / WRITE_SIZE to bytes."""
@@ -313,6 +383,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--sampler", choices=["on", "off"], default="on")
+    ap.add_argument("--verify-round", choices=["on", "off"], default="on",
+                    help="also time a whole 36-layer verify round (forward graph, logits, fused accept)")
     ap.add_argument("--copy-probe", choices=["on", "off"], default="off",
                     help="also time a plain 1 GiB device copy (the counter scale for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -336,9 +408,11 @@ def main():
              "qk_norm_rope_store": qk_rope_bench(args, dev)}
     if args.sampler == "on":
         extra["sampler"] = sampler_bench(args, dev)
+    if args.verify_round == "on":
+        extra["verify_round"] = verify_round_bench(args, dev)
     if args.copy_probe == "on":
         extra["copy_probe"] = copy_probe(args, dev)
-    cpu =cpu_baseline(case) if args.cpu_baseline == "on" else None
+    cpu = cpu_baseline(case) if args.cpu_baseline == "on" else None
 
     result = {
         "metric": METRIC,

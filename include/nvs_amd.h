@@ -5,6 +5,8 @@
  *   1. paged multi-query verify attention (+ the paged KV store, and the fused q/k RMSNorm + RoPE + store, that
  *      precede it), and
  *   2. the speculative sampler: truncation -> softmax -> rejection test -> residual / bonus race.
+ * Two elementwise ops of the decoder layer (RMSNorm with the residual add, SiLU-and-mul) complete a verify forward
+ * around the library GEMMs.
  *
  * Every entry point takes plain device pointers, element strides and sizes, plus the HIP stream to launch on
  * (NULL = the legacy default stream). Nothing here allocates, synchronises the host with the device, or reads a
@@ -28,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NVS_ABI_VERSION 2
+#define NVS_ABI_VERSION 3
 
 typedef enum {
     NVS_OK = 0,
@@ -203,6 +205,27 @@ int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_str
                     int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
                     int64_t* n_accept, int64_t* tail, int32_t* row_counters,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------ decoder-layer elementwise ops
+ * The elementwise steps between the projections of a Qwen3 decoder layer, so that a whole verify forward runs
+ * on this library and the GEMMs (Qwen3DecoderLayer.forward, nanovllm/models/qwen3.py:146-160).
+ *
+ * nvs_rms_norm replaces RMSNorm.forward (nanovllm/layers/layernorm.py:15-46). Per row:
+ *   x' = float(x) (+ float(residual) when residual is non-NULL, and then residual = dtype(x'), written in place);
+ *   out = dtype(dtype(x' / sqrt(mean(x'^2) + eps)) * weight)   (the reference's explicit casts, one rounding each).
+ * x, residual, out: [n_rows, hidden] with the given row strides; weight [hidden]; dtype bf16 or fp16; hidden a
+ * multiple of 8, at most 8192; pointers 16-byte aligned and row strides multiples of 8 (NVS_ERR_UNSUPPORTED
+ * otherwise). out may alias x, not residual. The sum of squares is an fp32 sum in a fixed order. */
+int nvs_rms_norm(const void* x, int64_t x_row_stride, void* residual, int64_t residual_row_stride,
+                 const void* weight, float eps, void* out, int64_t out_row_stride, int64_t n_rows, int hidden,
+                 int dtype, void* stream);
+
+/* nvs_silu_and_mul replaces SiluAndMul.forward (nanovllm/layers/activation.py:8-11): per row of x = [gate | up],
+ * each of width elements, out = dtype(silu(gate) * up), computed in fp32 and rounded once (the reference runs it
+ * under torch.compile, which keeps the product in fp32). x [n_rows, 2 * width], out [n_rows, width]; dtype bf16 or
+ * fp16; width a multiple of 8; pointers 16-byte aligned and row strides multiples of 8. */
+int nvs_silu_and_mul(const void* x, int64_t x_row_stride, void* out, int64_t out_row_stride, int64_t n_rows,
+                     int width, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version_and_empty_error(lib):
-    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 3
     assert isinstance(lib.nvs_last_error(), bytes)
 
 
@@ -124,3 +124,30 @@ def test_qk_norm_rope_store_rejects_bad_arguments(lib):
     assert call(slots=1 << 26) == _lib.NVS_ERR_INVALID     # slots without caches
     assert call(n_cs=0) == _lib.NVS_ERR_INVALID
     assert call(T=0) == _lib.NVS_OK                        # nothing to do, nothing launched
+
+
+def test_rms_norm_and_silu_mul_reject_bad_arguments(lib):
+    def norm(**over):
+        a = dict(x=1 << 20, x_rs=4096, res=None, res_rs=0, w=1 << 21, eps=1e-6, out=1 << 22, out_rs=4096, rows=4,
+                 hidden=4096, dtype=_lib.DTYPE_BF16, stream=None)
+        a.update(over)
+        return lib.nvs_rms_norm(*a.values())
+    assert norm(dtype=_lib.DTYPE_F32) == _lib.NVS_ERR_UNSUPPORTED
+    assert norm(hidden=4100) == _lib.NVS_ERR_UNSUPPORTED      # not a multiple of 8
+    assert norm(hidden=16384, x_rs=16384, out_rs=16384) == _lib.NVS_ERR_UNSUPPORTED   # above 8192
+    assert norm(x_rs=2048) == _lib.NVS_ERR_INVALID            # shorter than the row
+    assert norm(res=1 << 23, res_rs=1000) == _lib.NVS_ERR_INVALID
+    assert norm(x=(1 << 20) + 2) == _lib.NVS_ERR_UNSUPPORTED  # not 16-byte aligned
+    assert norm(w=None) == _lib.NVS_ERR_INVALID
+    assert norm(rows=0) == _lib.NVS_OK                        # nothing to do, nothing launched
+
+    def silu(**over):
+        a = dict(x=1 << 20, x_rs=24576, out=1 << 22, out_rs=12288, rows=4, width=12288, dtype=_lib.DTYPE_BF16,
+                 stream=None)
+        a.update(over)
+        return lib.nvs_silu_and_mul(*a.values())
+    assert silu(dtype=_lib.DTYPE_F32) == _lib.NVS_ERR_UNSUPPORTED
+    assert silu(width=12) == _lib.NVS_ERR_UNSUPPORTED
+    assert silu(x_rs=12288) == _lib.NVS_ERR_INVALID           # holds the gate only
+    assert silu(out=None) == _lib.NVS_ERR_INVALID
+    assert silu(rows=0) == _lib.NVS_OK

@@ -1,0 +1,64 @@
+"""Host logic of the verify round, no GPU: the graphs' token counts (verify_schedule.py:18-23, with the known
+answers of the reference's tests/test_verify_schedule.py:54-55), the row-slot metadata (batch_metadata.py:149-181)
+on a hand-worked example, and the weight bytes of the Qwen3-8B shape."""
+import pytest
+
+from nvs_amd import verify_round as vr
+
+
+def test_token_counts_known_answers():
+    assert vr.verify_token_counts(4, 8) == [1, 2, 4, 8, 16, 24, 32]
+    assert all(b * 8 in vr.verify_token_counts(64, 8) for b in range(1, 65))
+    assert vr.verify_token_counts(3, 4) == [1, 2, 4, 8, 12]      # 4 is not below query_len 4: listed once
+    assert vr.verify_token_counts(2, 1) == [1, 2]
+
+
+def test_graph_shapes_cap_the_rows():
+    counts = vr.verify_token_counts(512, 8)
+    shapes = [(min(n, 512), n) for n in counts]
+    assert shapes[-1] == (512, 4096) and (288, 288) in shapes and (512, 520) in shapes
+
+
+def test_metadata_hand_worked():
+    # row 0 verifies 3 tokens at the end of 300 (positions 297..299 in its second block, physical block 2);
+    # row 1 verifies 1 token of 5 (position 4 in block 7). 8 token slots: one padding row of 4 tokens on the pad
+    # block (8), then an empty row.
+    batch = vr.VerifyBatch(q_lens=[3, 1], k_lens=[300, 5], block_tables=[[5, 2], [7]], num_blocks=8)
+    md = vr.verify_varlen_metadata(batch, num_rows=4, num_tokens=8, width=3, query_len=8)
+    assert md.positions == [297, 298, 299, 4, 0, 1, 2, 3]
+    assert md.slot_mapping == [2 * 256 + 41, 2 * 256 + 42, 2 * 256 + 43, 7 * 256 + 4, -1, -1, -1, -1]
+    assert md.cu_seqlens_q == [0, 3, 4, 8, 8]
+    assert md.cu_seqlens_k == [0, 300, 305, 309, 309]
+    assert md.block_tables == [[5, 2, 8], [7, 8, 8], [8, 8, 8], [8, 8, 8]]
+
+
+def test_metadata_padding_rows_hold_at_most_query_len():
+    batch = vr.VerifyBatch(q_lens=[1], k_lens=[10], block_tables=[[0]], num_blocks=1)
+    md = vr.verify_varlen_metadata(batch, num_rows=4, num_tokens=12, width=1, query_len=4)
+    assert md.cu_seqlens_q == [0, 1, 5, 9, 12]
+    assert md.slot_mapping[1:] == [-1] * 11
+    capture = vr.verify_varlen_metadata(None, num_rows=3, num_tokens=20, width=2, query_len=8, pad_block=5)
+    assert capture.cu_seqlens_q == [0, 8, 16, 20] and capture.block_tables == [[5, 5]] * 3
+
+
+def test_metadata_rejects_what_does_not_fit():
+    batch = vr.VerifyBatch(q_lens=[8, 8], k_lens=[100, 100], block_tables=[[0], [1]], num_blocks=2)
+    with pytest.raises(ValueError):
+        vr.verify_varlen_metadata(batch, num_rows=2, num_tokens=8, width=1, query_len=8)    # 16 tokens in 8
+    with pytest.raises(ValueError):
+        vr.verify_varlen_metadata(batch, num_rows=2, num_tokens=24, width=1, query_len=8)   # no padding row left
+    with pytest.raises(ValueError):
+        vr.verify_varlen_metadata(batch, num_rows=1, num_tokens=16, width=1, query_len=8)   # two rows, one slot
+    with pytest.raises(ValueError):
+        vr.verify_varlen_metadata(vr.VerifyBatch([9], [100], [[0]], 1), num_rows=2, num_tokens=16, width=1,
+                                  query_len=8)                                               # 9 > query_len
+
+
+def test_random_batch_and_weight_bytes():
+    batch = vr.random_verify_batch(64)
+    assert len(batch.q_lens) == 64 and all(1 <= q <= 8 for q in batch.q_lens)
+    assert all(2800 <= k <= 3200 for k in batch.k_lens)
+    blocks = sorted(b for t in batch.block_tables for b in t)
+    assert blocks == list(range(batch.num_blocks))                  # a permutation: every block used once
+    assert all(len(t) * 256 >= k for t, k in zip(batch.block_tables, batch.k_lens))
+    assert vr.QWEN3_8B.streamed_weight_bytes() == 15_136_194_560   # 36 layers + LM head in bf16
