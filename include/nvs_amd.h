@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NVS_ABI_VERSION 3
+#define NVS_ABI_VERSION 4
 
 typedef enum {
     NVS_OK = 0,
@@ -205,6 +205,30 @@ int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_str
                     int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
                     int64_t* n_accept, int64_t* tail, int32_t* row_counters,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ Markov draw
+ * Replaces one candidate row of DFlashDrafter._markov_rows (nanovllm/engine/speculative.py:163-184, the
+ * `elif candidates:` branch): for each of `batch` sequences, given that row's biased draft logits
+ * (logits[:, row] + markov_head(prev), computed by the caller as the reference does):
+ *   values, ids = topk(row_logits, num_candidates)            (ties in index order)
+ *   probs = probs_from_logits(values, sampling)                (temperature, top-k, top-p over the candidates)
+ *   token = ids[race(probs, noise[:, row])]                    (argmax of probs / noise, first rank on ties)
+ * and writes the sparse row instead of scattering it over the vocabulary: cand_ids[b, c] / cand_probs[b, c] for
+ * the candidates with a non-zero probability, in rank order, then id -1 and probability 0 up to num_candidates;
+ * draws[b * draws_stride] = token. Only the kept candidates are ranked: the others have probability 0 in the
+ * reference and never win its race unless every probability is 0 (then rank 0, the row's largest value).
+ * num_candidates is the reference's num_candidates() = min(max_top_k + 64, vocab); every row must truncate with
+ * top-k (the reference's candidate rows require it; a row with top_k <= 0 is drawn among its top max_top_k).
+ * logits [batch, vocab] fp32 / bf16 / fp16 with a row stride; noise [batch, >= num_candidates] fp32, the row's
+ * exponential noise by candidate rank; parameters per row as in nvs_probs_from_logits. min(max_top_k, vocab) <=
+ * num_candidates <= 7168.
+ * One launch per row of the draft block; the rows are sequential because each row's bias depends on the token
+ * drawn before it. */
+int nvs_markov_draw(const void* logits, int logits_dtype, int64_t logits_row_stride, int64_t batch, int64_t vocab,
+                    const float* temperatures, const int64_t* top_k, const float* top_p, int max_top_k,
+                    int has_top_p, int num_candidates, const float* noise, int64_t noise_row_stride,
+                    int32_t* cand_ids, float* cand_probs, int64_t cand_row_stride, int64_t* draws,
+                    int64_t draws_stride, void* stream);
 
 /* ------------------------------------------------------------------------------ decoder-layer elementwise ops
  * The elementwise steps between the projections of a Qwen3 decoder layer, so that a whole verify forward runs

@@ -36,7 +36,7 @@ constexpr int kCap = kSelWaves * kWaveSlots;   // LDS candidate capacity (8192)
 constexpr int kMaxTopK = 1024;
 constexpr int kRaceChunk = 16384;              // vocabulary chunk of the dense race kernels
 
-enum Mode { kModeAccept = 0, kModeProbs = 1, kModeTruncate = 2 };
+enum Mode { kModeAccept = 0, kModeProbs = 1, kModeTruncate = 2, kModeMarkov = 3 };
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -101,6 +101,14 @@ struct SelArgs {
     // dense outputs
     float* out;
     int64_t out_stride;
+    // Markov draw: candidates per position, noise by candidate rank, sparse outputs and the drawn token
+    int n_cand;
+    int64_t noise_stride;
+    int32_t* cand_ids;
+    float* cand_probs;
+    int64_t cand_stride;
+    int64_t* draws;
+    int64_t draws_stride;
 };
 
 // ---------------------------------------------------------------- wave / workgroup helpers
@@ -337,6 +345,7 @@ __device__ void block_sort_desc(SelShared& sh, int n) {
         }
     }
 }
+
 
 // Row locator of the fused accept: position t -> batch row b, draft index j, verified length L, first position.
 __device__ void locate(const SelArgs& a, int64_t t, SelShared& sh) {
@@ -753,6 +762,168 @@ __device__ __forceinline__ bool count_position(int* counter, int64_t n_positions
     return before == static_cast<int>(n_positions) - 1;
 }
 
+// ---------------------------------------------------------------- Markov draw (DSpark candidate rows)
+
+// (key, index) pairs of a Markov draw: key << 32 | ~index, so that a descending sort orders by value, then by
+// index ascending. They reuse the space of ckey and cidx (contiguous, 64 KB).
+constexpr int kPairCap = kCap;
+// Candidates of a Markov row: the pairs must hold the values above the threshold (fewer than max_top_k <= 1024)
+// and the ties taken after them.
+constexpr int kMaxCandidates = kPairCap - kMaxTopK;
+
+__device__ __forceinline__ uint64_t* pair_buf(SelShared& sh) { return reinterpret_cast<uint64_t*>(sh.ckey); }
+
+// Descending bitonic sort of buf[0..n) (n <= kPairCap), padded with zeros to a power of two.
+__device__ void block_sort_desc_u64(uint64_t* buf, int n) {
+    int p = 64;
+    while (p < n) p <<= 1;
+    for (int i = n + threadIdx.x; i < p; i += blockDim.x) buf[i] = 0ull;
+    __syncthreads();
+    for (int size = 2; size <= p; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < p / 2; i += blockDim.x) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const uint64_t x = buf[lo], y = buf[hi];
+                const bool desc = ((lo & size) == 0);
+                if (desc ? (x < y) : (x > y)) {
+                    buf[lo] = y;
+                    buf[hi] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Exclusive prefix over the workgroup in thread order; *total gets the sum (every thread).
+__device__ int block_scan_excl(int v, SelShared& sh, int* total) {
+    const int incl = wave_scan_incl_dpp(v);
+    __syncthreads();
+    if (lane_id() == 63) sh.wcount[threadIdx.x >> 6] = incl;
+    __syncthreads();
+    int before = 0, all = 0;
+    for (int w = 0; w < kSelWaves; ++w) {
+        const int c = sh.wcount[w];
+        before += (w < static_cast<int>(threadIdx.x >> 6)) ? c : 0;
+        all += c;
+    }
+    *total = all;
+    return before + incl - v;
+}
+
+// One past the index of the need-th value (1-based, in index order) whose key equals tie_key; the vocabulary size
+// when the row has fewer. Within a batch, value slot vi of thread x holds element
+// e0 + ((vi / W) * kSelThreads + x) * W + vi % W, so index order is (slot group, thread, slot in group).
+template <int DT, bool VEC>
+__device__ int64_t nth_tie_end(const SelArgs& a, const char* row, float temp, bool unit_temp, uint32_t tie_key,
+                               int need, SelShared& sh) {
+    constexpr int W = piece_elems<DT>();
+    if (need <= 0) return 0;
+    int seen = 0;
+    for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
+        float v[kVpt];
+        load_vals<DT, VEC>(row, e0, a.vocab, v);
+#pragma unroll
+        for (int g = 0; g < kVpt / W; ++g) {
+            int mine = 0;
+#pragma unroll
+            for (int c = 0; c < W; ++c) mine += (sel_key(scale_logit(v[g * W + c], temp, unit_temp)) == tie_key);
+            int total = 0;
+            const int before = block_scan_excl(mine, sh, &total);
+            if (seen + total >= need) {
+                // the need-th tie is in this slot group: the thread holding it reports its index
+                int r = seen + before;
+#pragma unroll
+                for (int c = 0; c < W; ++c) {
+                    if (sel_key(scale_logit(v[g * W + c], temp, unit_temp)) == tie_key && ++r == need)
+                        sh.loc[3] = val_index<DT>(e0, g * W + c) + 1;
+                }
+                __syncthreads();
+                return sh.loc[3];
+            }
+            seen += total;
+        }
+    }
+    return a.vocab;
+}
+
+// DSpark's Markov row (speculative.py:173-180) for one position, after the row statistics: the candidates are
+// the kept values (key >= theta_key) in (value descending, index ascending) order, at most n_cand of them; their
+// probabilities exp(s - m) / Z with Z over the candidates; the race argmax_c p_c / noise[c] by candidate rank, the
+// first rank on ties, rank 0 when every score is zero; the drawn token and the sparse row (ids, probs), with
+// id -1 and probability 0 past the candidates.
+template <int DT, bool VEC>
+__device__ void markov_tail(const SelArgs& a, int64_t t, const char* row, float temp, bool unit_temp,
+                            uint32_t theta_key, SelShared& sh) {
+    uint64_t* pairs = pair_buf(sh);
+    const int C = a.n_cand;
+    auto collect = [&](int64_t tie_end) {
+        if (threadIdx.x == 0) {
+            sh.count = 0;
+            sh.bin_count = 0;
+        }
+        __syncthreads();
+        for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
+            float v[kVpt];
+            load_vals<DT, VEC>(row, e0, a.vocab, v);
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) {
+                const uint32_t key = sel_key(scale_logit(v[vi], temp, unit_temp));
+                const int64_t e = val_index<DT>(e0, vi);
+                if (key == 0u || key < theta_key || (key == theta_key && e >= tie_end)) continue;
+                const int p = atomicAdd(&sh.count, 1);
+                if (key > theta_key) atomicAdd(&sh.bin_count, 1);
+                if (p < kPairCap)
+                    pairs[p] = (static_cast<uint64_t>(key) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
+            }
+        }
+        __syncthreads();
+    };
+    collect(a.vocab);
+    int n = sh.count;
+    if (n > kPairCap) {
+        // Only ties at theta make that many: the values above it are fewer than the rank. The candidates are
+        // those values and the first ties in index order.
+        const int need = max(C - sh.bin_count, 0);
+        const int64_t tie_end = nth_tie_end<DT, VEC>(a, row, temp, unit_temp, theta_key, need, sh);
+        collect(tie_end);
+        n = sh.count;
+    }
+    block_sort_desc_u64(pairs, n);
+    const int nc = min(n, C);
+    const float m = nc > 0 ? nvs::key_float(static_cast<uint32_t>(pairs[0] >> 32)) : 0.f;
+    float z = 0.f;
+    for (int c = threadIdx.x; c < nc; c += blockDim.x) z += expf(nvs::key_float(static_cast<uint32_t>(pairs[c] >> 32)) - m);
+    z = block_sum(z, sh);
+    int32_t* ids = a.cand_ids + t * a.cand_stride;
+    float* probs = a.cand_probs + t * a.cand_stride;
+    const float* noise = a.noise + t * a.noise_stride;
+    uint64_t best = 0;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float p = 0.f;
+        int32_t id = -1;
+        if (c < nc) {
+            const uint64_t pr = pairs[c];
+            p = expf(nvs::key_float(static_cast<uint32_t>(pr >> 32)) - m) / z;
+            id = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(pr));
+        }
+        ids[c] = id;
+        probs[c] = p;
+        const float score = p / noise[c];
+        const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+                             static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(c));
+        best = best > k64 ? best : k64;
+    }
+    best = block_max_u64(best, sh);
+    if (threadIdx.x == 0) {
+        const float score = nvs::key_float(static_cast<uint32_t>(best >> 32));
+        const int win = (score > 0.f) ? static_cast<int>(0xffffffffu - static_cast<uint32_t>(best)) : 0;
+        a.draws[t * a.draws_stride] =
+            win < nc ? static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(pairs[win])) : int64_t{0};
+    }
+}
+
 template <int DT, int MODE, bool VEC>
 // At most 128 VGPRs (4 waves per SIMD): two 8-wave workgroups per CU, so the 512 positions of a verify batch
 // run in one round on 256 CUs.
@@ -781,8 +952,11 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
     const int64_t tk = a.top_k != nullptr ? a.top_k[prow] : 0;
     const float top_p = a.top_p != nullptr ? a.top_p[prow] : 1.f;
     const int K = static_cast<int>(min(static_cast<int64_t>(a.max_top_k), a.vocab));
-    const bool truncating = K > 0 && tk > 0;
-    const int rank = truncating ? static_cast<int>(min(tk, static_cast<int64_t>(K))) : 0;
+    // A Markov draw always truncates (every row of a candidate batch has top-k); a row without top-k there is
+    // drawn among its top max_top_k.
+    const bool truncating = K > 0 && (tk > 0 || MODE == kModeMarkov);
+    const int rank = truncating ? static_cast<int>(min(tk > 0 ? tk : static_cast<int64_t>(K),
+                                                       static_cast<int64_t>(K))) : 0;
     const char* row = static_cast<const char*>(a.logits) + t * a.row_stride * nvs::dtype_size(DT);
 
     // Fused accept: the accept test's inputs (draft token d, the logit at d, q at d, the uniform) do not depend on
@@ -1298,7 +1472,10 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
     const uint32_t theta_key = rs.theta == -INFINITY ? 0u : nvs::float_key(rs.theta);
     const float mu = (rs.m == -INFINITY) ? 0.f : rs.m;
 
-    if constexpr (MODE == kModeProbs || MODE == kModeTruncate) {
+    if constexpr (MODE == kModeMarkov) {
+        markov_tail<DT, VEC>(a, t, row, temp, unit_temp, theta_key, sh);
+        return;
+    } else if constexpr (MODE == kModeProbs || MODE == kModeTruncate) {
         float* orow = a.out + t * a.out_stride;
         for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
             float v[kVpt];
@@ -1680,6 +1857,52 @@ extern "C" int nvs_truncate_logits(const float* scaled, int64_t scaled_row_strid
     a.out = out;
     a.out_stride = vocab;
     return launch_select<kModeTruncate>(NVS_DTYPE_F32, a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t logits_row_stride, int64_t batch,
+                               int64_t vocab, const float* temperatures, const int64_t* top_k, const float* top_p,
+                               int max_top_k, int has_top_p, int num_candidates, const float* noise,
+                               int64_t noise_row_stride, int32_t* cand_ids, float* cand_probs,
+                               int64_t cand_row_stride, int64_t* draws, int64_t draws_stride, void* stream) {
+    nvs::clear_error();
+    int st = check_dtype(logits_dtype);
+    if (st != NVS_OK) return st;
+    st = common_select_checks(logits, logits_row_stride, batch, vocab, 1, max_top_k, top_k);
+    if (st != NVS_OK) return st;
+    NVS_CHECK(max_top_k >= 1, NVS_ERR_INVALID, "markov_draw: candidate rows need top-k (max_top_k >= 1)");
+    NVS_CHECK(num_candidates <= kMaxCandidates, NVS_ERR_UNSUPPORTED,
+              "markov_draw: num_candidates %d above %d", num_candidates, kMaxCandidates);
+    NVS_CHECK(num_candidates >= 1 && num_candidates >= min(static_cast<int64_t>(max_top_k), vocab), NVS_ERR_INVALID,
+              "markov_draw: num_candidates %d below min(max_top_k, vocab): the candidates must hold the top-k",
+              num_candidates);
+    NVS_CHECK(temperatures != nullptr, NVS_ERR_INVALID, "markov_draw: temperatures is NULL (greedy rows use argmax)");
+    NVS_CHECK(!has_top_p || top_p != nullptr, NVS_ERR_INVALID, "markov_draw: has_top_p needs top_p");
+    NVS_CHECK(batch == 0 || (noise && cand_ids && cand_probs && draws), NVS_ERR_INVALID,
+              "markov_draw: null noise, cand_ids, cand_probs or draws");
+    NVS_CHECK(noise_row_stride >= num_candidates && cand_row_stride >= num_candidates, NVS_ERR_INVALID,
+              "markov_draw: a row stride is shorter than num_candidates");
+    NVS_CHECK(draws_stride >= 1, NVS_ERR_INVALID, "markov_draw: draws_stride must be >= 1");
+    if (batch == 0) return NVS_OK;
+    SelArgs a{};
+    a.logits = logits;
+    a.row_stride = logits_row_stride;
+    a.n_pos = batch;
+    a.vocab = vocab;
+    a.temps = temperatures;
+    a.top_k = top_k;
+    a.top_p = top_p;
+    a.max_top_k = max_top_k;
+    a.has_top_p = has_top_p;
+    a.pos_per_param = 1;
+    a.noise = noise;
+    a.noise_stride = noise_row_stride;
+    a.n_cand = num_candidates;
+    a.cand_ids = cand_ids;
+    a.cand_probs = cand_probs;
+    a.cand_stride = cand_row_stride;
+    a.draws = draws;
+    a.draws_stride = draws_stride;
+    return launch_select<kModeMarkov>(logits_dtype, a, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int nvs_race_workspace_size(int64_t n_rows, int64_t vocab, size_t* bytes) {

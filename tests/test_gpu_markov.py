@@ -1,0 +1,140 @@
+"""DSpark's Markov rows on the GPU against the oracle (oracle/markov.py), through nvs_markov_draw.
+
+The Markov bias is a lookup table by previous token (as the reference's tests/test_dspark_propose.py passes it),
+so the GPU and the CPU oracle add identical biases whenever they drew identical tokens.
+Bar: drafts bit-exact, candidate ids bit-exact, the number of kept candidates equal, probabilities within 1e-5 of
+their value (the kernel's exp and its sum order differ from torch's softmax). Cases: the reference's propose tests,
+random rows at V = 4,096 (fp32) and 151,936 (bf16) with mixed temperatures / top-k / top-p, ties at the cut inside
+and beyond the candidates (the kernel's ordered tie pass), a dense batch (a row without top-k), and the sparse rows
+scattered back to the reference's dense q.
+"""
+import pytest
+import torch
+
+from conftest import log_case
+from nvs_amd.layers import markov as nm
+from nvs_amd.layers import spec_sampler as ns
+from oracle import markov as om
+from oracle import spec_sampler as ss
+
+pytestmark = pytest.mark.gpu
+
+
+def sampling(device, temps, top_k, top_p):
+    t = None if temps is None else torch.tensor(temps, dtype=torch.float32, device=device)
+    k = torch.tensor(top_k, dtype=torch.int64, device=device)
+    p = torch.tensor(top_p, dtype=torch.float32, device=device)
+    return ns.SamplingTensors(t, k, p, int(k.max()), bool((p < 1).any()), bool((k > 0).all()))
+
+
+def run_both(device, logits, anchors, table, st, seed=0):
+    """The product's sample_markov on the GPU and the oracle on the CPU with the same noise."""
+    bias = lambda prev: table[prev % table.shape[0]]
+    gen = torch.Generator(device=device).manual_seed(seed)
+    lg = logits.to(device)
+    tab = table.to(device)
+    drafts, q = nm.sample_markov(lg, anchors.to(device), st, lambda prev: tab[prev % tab.shape[0]], gen)
+    torch.cuda.synchronize()
+    batch, k, vocab = logits.shape
+    cands = nm.num_candidates(st.max_top_k, st.all_top_k, vocab)
+    noise = None
+    if st.temperatures is not None:
+        gen.manual_seed(seed)                        # the product's draw, replayed for the oracle
+        noise = ns.exponential_noise_(torch.empty(batch, k, cands or vocab, device=device), gen).cpu()
+    cpu = lambda t: None if t is None else t.cpu()
+    want = om.markov_rows(logits, anchors, bias, cpu(st.temperatures), cpu(st.top_k), cpu(st.top_p), st.max_top_k,
+                          st.has_top_p, st.all_top_k, noise)
+    return drafts.cpu(), q, want
+
+
+def check_candidates(q, want, what):
+    _, _, ids_ref, probs_ref = want
+    ids, probs = q.ids.cpu().long(), q.probs.cpu()
+    live = ids >= 0
+    kept_ref = probs_ref > 0
+    assert torch.equal(live.sum(-1), kept_ref.sum(-1)), f"{what}: kept counts differ"
+    assert torch.equal(ids[live], ids_ref[live]), f"{what}: candidate ids differ"
+    assert bool((probs[~live] == 0).all())
+    assert torch.allclose(probs, probs_ref, rtol=1e-5, atol=1e-7), \
+        f"{what}: max prob diff {float((probs - probs_ref).abs().max()):.3e}"
+
+
+def test_reference_propose_cases(device):
+    log_case("markov rows: reference propose cases")
+    bias = torch.tensor([[0.0, 2.0, 0.0], [0.0, 0.0, 0.0], [0.0, 0.0, 0.0]])
+    logits = torch.tensor([2.0, 1.0, 0.0]).expand(2, 3, 3).contiguous()
+    drafts, q, _ = run_both(device, logits, torch.tensor([0, 1]), bias, sampling(device, None, [0, 0], [1.0, 1.0]))
+    assert drafts.tolist() == [[1, 0, 1], [0, 1, 0]] and q is None
+    # every row truncates: candidate rows over 84 of 200 tokens, thirty ties at the cut value 3
+    vocab = 200
+    logits = torch.randn(2, 4, vocab, generator=torch.Generator().manual_seed(5))
+    logits[0] = logits[0].clamp(max=2.5)
+    logits[0, :, :32] = torch.tensor([5.0, 4.0] + [3.0] * 30)
+    st = sampling(device, [0.7, 1.0], [3, 20], [1.0, 0.8])
+    drafts, q, want = run_both(device, logits, torch.tensor([2, 0]), torch.zeros(1, vocab), st)
+    assert isinstance(q, nm.CandidateRows) and q.ids.shape == (2, 4, 84)
+    assert torch.equal(drafts, want[0])
+    check_candidates(q, want, "ties at the cut")
+    dense = q.to_dense(vocab).cpu()
+    assert torch.equal(dense > 0, want[1] > 0) and torch.allclose(dense, want[1], rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("vocab, dtype, batch", [(4096, torch.float32, 16), (151936, torch.bfloat16, 8)])
+def test_random_rows_match_the_oracle(device, vocab, dtype, batch):
+    log_case(f"markov rows: random V={vocab} {dtype} B={batch}")
+    g = torch.Generator().manual_seed(vocab)
+    logits = (torch.randn(batch, 7, vocab, generator=g) * 3).to(dtype)
+    table = (torch.randn(16, vocab, generator=g) * 2).to(dtype)
+    temps = [1.0, 0.7, 1.3, 1.0] * (batch // 4)
+    top_k = [20, 5, 50, 1] * (batch // 4)
+    top_p = [1.0, 0.8, 0.95, 1.0] * (batch // 4)
+    st = sampling(device, temps, top_k, top_p)
+    anchors = torch.randint(0, vocab, (batch,), generator=g)
+    drafts, q, want = run_both(device, logits, anchors, table, st, seed=1)
+    assert torch.equal(drafts, want[0]), f"drafts differ at {(drafts != want[0]).nonzero()[:5].tolist()}"
+    check_candidates(q, want, "random rows")
+
+
+@pytest.mark.parametrize("ties", [5000, 20000])
+def test_ties_beyond_the_candidates(device, ties):
+    # ten distinct top values, then `ties` copies of the 11th; top-k 11 keeps them all, the candidates keep the
+    # first 65 of them in index order (20,000 ties exceed the kernel's pair list: its ordered tie pass)
+    log_case(f"markov rows: {ties} ties at the cut")
+    vocab = 151936
+    g = torch.Generator().manual_seed(ties)
+    logits = torch.randn(2, 2, vocab, generator=g).clamp(max=3.0)
+    where = torch.randperm(vocab, generator=g)
+    logits[:, :, where[:10]] = torch.arange(20.0, 10.0, -1.0)
+    logits[:, :, where[10:10 + ties]] = 5.0
+    st = sampling(device, [1.0, 0.9], [11, 11], [1.0, 1.0])
+    drafts, q, want = run_both(device, logits, torch.tensor([0, 1]), torch.zeros(1, vocab), st, seed=2)
+    assert torch.equal(drafts, want[0])
+    check_candidates(q, want, f"{ties} ties")
+    assert int((q.ids[0, 0] >= 0).sum()) == 75
+
+
+def test_dense_rows_when_some_row_does_not_truncate(device):
+    log_case("markov rows: dense batch")
+    vocab = 3000
+    g = torch.Generator().manual_seed(7)
+    logits = torch.randn(4, 3, vocab, generator=g) * 2
+    table = torch.randn(8, vocab, generator=g)
+    st = sampling(device, [1.0, 0.8, 1.0, 1.2], [0, 10, 40, 5], [1.0, 0.9, 1.0, 1.0])
+    drafts, q, want = run_both(device, logits, torch.tensor([1, 2, 3, 4]), table, st, seed=3)
+    assert torch.equal(drafts, want[0])
+    assert torch.allclose(q.cpu(), want[1], rtol=1e-5, atol=1e-7)
+
+
+def test_markov_draw_rejects_bad_arguments(device):
+    st = sampling(device, [1.0], [20], [1.0])
+    lg = torch.zeros(1, 100, device=device)
+    ids = torch.empty(1, 84, dtype=torch.int32, device=device)
+    probs = torch.empty(1, 84, device=device)
+    noise = torch.ones(1, 84, device=device)
+    draws = torch.empty(1, dtype=torch.int64, device=device)
+    with pytest.raises(Exception):
+        nm.markov_draw(lg, st, 10, noise, ids, probs, draws)          # fewer candidates than max_top_k
+    with pytest.raises(ValueError):
+        nm.markov_draw(lg, st, 84, noise, ids.long(), probs, draws)
+    with pytest.raises(ValueError):
+        nm.markov_draw(lg, sampling(device, None, [20], [1.0]), 84, noise, ids, probs, draws)
