@@ -165,12 +165,26 @@ def sampler_bench(args, dev):
         ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st_p, None, g.uniforms, g.noise, workspace=ws)
 
     msp = time_gpu(step_p, max(10, args.steps // 2), max(3, args.warmup // 2))
+    # the same accept with q as DSpark candidate rows (top-64 + 64 = 128 entries per draft row) instead of dense
+    from nvs_amd.layers.markov import CandidateRows
+    top = g.q.topk(128, dim=-1)
+    rows = CandidateRows(top.indices.to(torch.int32).contiguous(), top.values.contiguous())
+
+    def step_c():
+        ns.spec_accept_with_draws(g.logits, rows, g.drafts, st, None, g.uniforms, g.noise, workspace=ws)
+
+    msc = time_gpu(step_c, max(10, args.steps // 2), max(3, args.warmup // 2))
+    same = [torch.equal(x, y) for x, y in zip(ns.spec_accept_with_draws(g.logits, rows, g.drafts, st, None, g.uniforms,
+                                                                        g.noise, workspace=ws), (n, tail))]
     log(f"[bench] fused sampler on bf16 logits: {ms16 * 1e3:.1f} us; top-p 0.9 + temperature 0.7: "
-        f"{msp * 1e3:.1f} us; greedy accept (fp32): {msg * 1e3:.1f} us")
+        f"{msp * 1e3:.1f} us; greedy accept (fp32): {msg * 1e3:.1f} us; q as candidate rows: {msc * 1e3:.1f} us "
+        f"(same decisions: {all(same)})")
     variants = {
         "topp0.9_temp0.7": {"us": round(msp * 1e3, 2), "GBs": round(alg / (msp * 1e-3) / 1e9, 1)},
         "bf16_logits": {"us": round(ms16 * 1e3, 2), "GBs": round(alg / 2 / (ms16 * 1e-3) / 1e9, 1),
                         "algorithmic_bytes": alg // 2},
+        "candidate_rows_q": {"us": round(msc * 1e3, 2), "GBs": round(alg / (msc * 1e-3) / 1e9, 1),
+                             "candidates": 128, "same_decisions_as_dense_q": all(same)},
         "greedy_fp32": {"us": round(msg * 1e3, 2), "GBs": round(alg / (msg * 1e-3) / 1e9, 1),
                         "algorithmic_bytes": alg, "kernel": "argmax_kernel + greedy_finalize_kernel"},
     }

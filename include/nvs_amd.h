@@ -206,6 +206,20 @@ int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_str
                     int64_t* n_accept, int64_t* tail, int32_t* row_counters,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* nvs_spec_accept with the draft q as candidate rows (the sparse rows nvs_markov_draw writes) instead of a dense
+ * [batch, num_drafts, vocab] tensor: q[b, j, v] = cand_probs[(b * num_drafts + j) * cand_row_stride + c] where
+ * cand_ids[...same...] == v (c < num_candidates; id -1 holds no token), else 0. The same decisions as
+ * nvs_spec_accept on the scattered q (the reference's draft_probs, speculative.py:169-180). Every row truncates
+ * with top-k (max_top_k >= 1; a row with top_k <= 0 is treated as top-k max_top_k), as DSpark's candidate batches
+ * do. */
+int nvs_spec_accept_candidates(const void* logits, int logits_dtype, int64_t logits_row_stride,
+                               const float* temperatures, const int64_t* top_k, const float* top_p, int max_top_k,
+                               int has_top_p, const int32_t* cand_ids, const float* cand_probs, int num_candidates,
+                               int64_t cand_row_stride, const int64_t* drafts, const int64_t* verified_lens,
+                               const float* uniforms, const float* noise, int64_t batch, int num_drafts,
+                               int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail,
+                               int32_t* row_counters, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ Markov draw
  * Replaces one candidate row of DFlashDrafter._markov_rows (nanovllm/engine/speculative.py:163-184, the
  * `elif candidates:` branch): for each of `batch` sequences, given that row's biased draft logits

@@ -87,7 +87,11 @@ struct SelArgs {
     int has_top_p;
     int64_t pos_per_param;
     // fused accept
-    const float* q;
+    const float* q;          // dense q [batch, k, vocab], or null with candidate rows below
+    const int32_t* q_ids;    // candidate rows of q: [batch * k, q_stride] token ids (-1: none) ...
+    const float* q_probs;    // ... and their probabilities
+    int q_cand;
+    int64_t q_stride;
     const int64_t* drafts;
     const int64_t* lens;
     const float* uniforms;
@@ -762,6 +766,150 @@ __device__ __forceinline__ bool count_position(int* counter, int64_t n_positions
     return before == static_cast<int>(n_positions) - 1;
 }
 
+// ---------------------------------------------------------------- q as candidate rows
+// A draft row's q given as candidate rows (DSpark's candidate rows, written by nvs_markov_draw): token ids
+// ids[slot * q_stride + c] with probabilities probs[...], c < q_cand, id -1 for no token. q(token) is the
+// probability of the entry holding the token, 0 when none does (the reference scatters the rows over a zeroed
+// [B, k, V] q, speculative.py:169-180).
+
+// q(token) by one whole wave: every lane checks every 64th entry; the first entry holding the token wins.
+__device__ float sparse_q_wave(const SelArgs& a, int64_t slot, int64_t token) {
+    const int32_t* ids = a.q_ids + slot * a.q_stride;
+    const float* probs = a.q_probs + slot * a.q_stride;
+    const int l = lane_id();
+    float found = 0.f;
+    int at = 0x7fffffff;
+    for (int c0 = 0; c0 < a.q_cand; c0 += 64) {
+        const int c = c0 + l;
+        const bool in = c < a.q_cand;
+        const int32_t id = in ? ids[c] : -1;
+        const float p = in ? probs[c] : 0.f;
+        if (id >= 0 && id == token && c < at) {
+            found = p;
+            at = c;
+        }
+    }
+    const int first = 0x7fffffff - static_cast<int>(wave_max_u32(static_cast<uint32_t>(0x7fffffff - at)));
+    if (first == 0x7fffffff) return 0.f;
+    const uint64_t who = __ballot(at == first);
+    return __shfl(found, static_cast<int>(__ffsll(static_cast<long long>(who))) - 1);
+}
+
+// q at each lane's kSelWaves tokens: every entry of the row is broadcast across the wave (64 at a time).
+__device__ void sparse_q_wave8(const SelArgs& a, int64_t slot, const int32_t (&tok)[kSelWaves],
+                               float (&q)[kSelWaves]) {
+    const int32_t* ids = a.q_ids + slot * a.q_stride;
+    const float* probs = a.q_probs + slot * a.q_stride;
+    const int l = lane_id();
+    bool done[kSelWaves];
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) {
+        q[w] = 0.f;
+        done[w] = false;
+    }
+    for (int c0 = 0; c0 < a.q_cand; c0 += 64) {
+        const int c = c0 + l;
+        const bool in = c < a.q_cand;
+        const int32_t id = in ? ids[c] : -1;
+        const float p = in ? probs[c] : 0.f;
+        const int n = min(64, a.q_cand - c0);
+        for (int src = 0; src < n; ++src) {
+            const int32_t bid = __builtin_amdgcn_readlane(id, src);
+            const float bp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), src));
+#pragma unroll
+            for (int w = 0; w < kSelWaves; ++w) {
+                const bool hit = !done[w] && bid >= 0 && tok[w] == bid;
+                q[w] = hit ? bp : q[w];
+                done[w] = done[w] || hit;
+            }
+        }
+    }
+}
+
+// q(token) by one thread, scanning the row (rows with more candidates than the hash holds).
+__device__ float sparse_q_scan(const SelArgs& a, int64_t slot, int64_t token) {
+    const int32_t* ids = a.q_ids + slot * a.q_stride;
+    const float* probs = a.q_probs + slot * a.q_stride;
+    for (int c = 0; c < a.q_cand; ++c)
+        if (ids[c] >= 0 && ids[c] == token) return probs[c];
+    return 0.f;
+}
+
+// Open-addressing hash of a row's tokens in the refinement histograms' space (free once the row statistics are
+// known): keys (token + 1, 0 = empty) in the first kQHash words, probabilities in the next kQHash. At most
+// kQHash / 2 entries, so every probe sequence meets an empty slot.
+constexpr int kQHash = 1024;
+static_assert(2 * kQHash <= kSelWaves * 256, "the hash must fit the refinement histograms");
+
+__device__ __forceinline__ uint32_t q_hash(int64_t token) {
+    return (static_cast<uint32_t>(token) * 2654435761u) >> 22;   // 10 bits
+}
+
+__device__ void build_q_hash(const SelArgs& a, int64_t slot, SelShared& sh) {
+    uint32_t* keys = &sh.whist[0][0];
+    uint32_t* vals = keys + kQHash;
+    for (int i = threadIdx.x; i < kQHash; i += blockDim.x) keys[i] = 0u;
+    __syncthreads();
+    const int32_t* ids = a.q_ids + slot * a.q_stride;
+    const float* probs = a.q_probs + slot * a.q_stride;
+    for (int c = threadIdx.x; c < a.q_cand; c += blockDim.x) {
+        const int32_t id = ids[c];
+        if (id < 0) continue;
+        const uint32_t key = static_cast<uint32_t>(id) + 1u;
+        uint32_t h = q_hash(id);
+        for (int probe = 0; probe < kQHash; ++probe) {
+            const uint32_t was = atomicCAS(&keys[h], 0u, key);
+            if (was == 0u) {
+                vals[h] = __float_as_uint(probs[c]);
+                break;
+            }
+            h = (h + 1u) & (kQHash - 1);
+        }
+    }
+    __syncthreads();
+}
+
+// The same hash built by one wave alone (the wave-0 finish, while the other waves wait): LDS operations of one wave
+// take effect in program order, so the lookups that follow see every insert.
+__device__ void build_q_hash_wave(const SelArgs& a, int64_t slot, SelShared& sh) {
+    uint32_t* keys = &sh.whist[0][0];
+    uint32_t* vals = keys + kQHash;
+    const int32_t* ids = a.q_ids + slot * a.q_stride;
+    const float* probs = a.q_probs + slot * a.q_stride;
+    for (int i = lane_id(); i < kQHash; i += 64) keys[i] = 0u;
+    compiler_fence_s();
+    for (int c = lane_id(); c < a.q_cand; c += 64) {
+        const int32_t id = ids[c];
+        const float pr = probs[c];
+        if (id < 0) continue;
+        const uint32_t key = static_cast<uint32_t>(id) + 1u;
+        uint32_t h = q_hash(id);
+        for (int probe = 0; probe < kQHash; ++probe) {
+            const uint32_t was = atomicCAS(&keys[h], 0u, key);
+            if (was == 0u) {
+                vals[h] = __float_as_uint(pr);
+                break;
+            }
+            h = (h + 1u) & (kQHash - 1);
+        }
+    }
+    compiler_fence_s();
+}
+
+__device__ float q_hash_lookup(SelShared& sh, int64_t token) {
+    const uint32_t* keys = &sh.whist[0][0];
+    const uint32_t* vals = keys + kQHash;
+    const uint32_t key = static_cast<uint32_t>(token) + 1u;
+    uint32_t h = q_hash(token);
+    for (int probe = 0; probe < kQHash; ++probe) {
+        const uint32_t k = keys[h];
+        if (k == key) return __uint_as_float(vals[h]);
+        if (k == 0u) return 0.f;
+        h = (h + 1u) & (kQHash - 1);
+    }
+    return 0.f;
+}
+
 // ---------------------------------------------------------------- Markov draw (DSpark candidate rows)
 
 // (key, index) pairs of a Markov draw: key << 32 | ~index, so that a descending sort orders by value, then by
@@ -952,9 +1100,9 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
     const int64_t tk = a.top_k != nullptr ? a.top_k[prow] : 0;
     const float top_p = a.top_p != nullptr ? a.top_p[prow] : 1.f;
     const int K = static_cast<int>(min(static_cast<int64_t>(a.max_top_k), a.vocab));
-    // A Markov draw always truncates (every row of a candidate batch has top-k); a row without top-k there is
-    // drawn among its top max_top_k.
-    const bool truncating = K > 0 && (tk > 0 || MODE == kModeMarkov);
+    // A Markov draw, and an accept whose q comes as candidate rows, always truncate (every row of a candidate
+    // batch has top-k); a row without top-k there is treated as top-k max_top_k.
+    const bool truncating = K > 0 && (tk > 0 || MODE == kModeMarkov || (MODE == kModeAccept && a.q_ids != nullptr));
     const int rank = truncating ? static_cast<int>(min(tk > 0 ? tk : static_cast<int64_t>(K),
                                                        static_cast<int64_t>(K))) : 0;
     const char* row = static_cast<const char*>(a.logits) + t * a.row_stride * nvs::dtype_size(DT);
@@ -976,7 +1124,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         if constexpr (MODE == kModeAccept) {
             const int64_t dc = min(max(dec_d, int64_t{0}), a.vocab - 1);
             dec_x = nvs::load_as_float<DT>(row, dc);
-            dec_q = a.q[dec_slot * a.vocab + dc];
+            dec_q = a.q_ids == nullptr ? a.q[dec_slot * a.vocab + dc] : 0.f;   // candidate rows: found later
             dec_u = a.uniforms[dec_slot];
         }
     };
@@ -1347,20 +1495,39 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                     const int kd = a.k;
                     const bool bonus = (j >= L - 1) || (j >= kd);
                     int acc = 0;
+                    // candidate rows of q: wave 0 hashes this draft row's tokens into the refinement histograms'
+                    // space (free once the threshold is known); rows with more candidates are broadcast instead
+                    const bool sparse = a.q_ids != nullptr;
+                    const bool whash = sparse && !bonus && a.q_cand <= kQHash / 2;
+                    if (whash) build_q_hash_wave(a, b * kd + j, sh);
+                    float dq = dec_q;
+                    if (sparse && dec_valid) dq = whash ? q_hash_lookup(sh, dec_d) : sparse_q_wave(a, dec_slot, dec_d);
                     if (lane == 0 && dec_valid) {
                         const float sd = scale_logit(dec_x, temp, unit_temp);
                         const float pd = (sel_key(sd) >= theta_key && sel_key(sd) != 0u) ? expf(sd - mu_f) / z : 0.f;
-                        acc = (dec_u * dec_q < pd) ? 1 : 0;
+                        acc = (dec_u * dq < pd) ? 1 : 0;
                     }
-                    const float* qrow = a.q + (b * kd + (bonus ? 0 : j)) * a.vocab;
                     const float* erow = a.noise + b * a.vocab;
                     // every load first (index 0 stands in for a pair that is not kept), then the scores
                     float qv[kSelWaves], ev[kSelWaves];
+                    int32_t tok[kSelWaves];
 #pragma unroll
                     for (int w = 0; w < kSelWaves; ++w) {
-                        const int64_t ix = kk[w] >= theta_key ? static_cast<int64_t>(ki[w]) : int64_t{0};
-                        qv[w] = bonus ? 0.f : qrow[ix];
-                        ev[w] = erow[ix];
+                        tok[w] = kk[w] >= theta_key ? ki[w] : 0;
+                        ev[w] = erow[tok[w]];
+                    }
+                    if (bonus) {
+#pragma unroll
+                        for (int w = 0; w < kSelWaves; ++w) qv[w] = 0.f;
+                    } else if (whash) {
+#pragma unroll
+                        for (int w = 0; w < kSelWaves; ++w) qv[w] = q_hash_lookup(sh, tok[w]);
+                    } else if (sparse) {
+                        sparse_q_wave8(a, b * kd + j, tok, qv);
+                    } else {
+                        const float* qrow = a.q + (b * kd + j) * a.vocab;
+#pragma unroll
+                        for (int w = 0; w < kSelWaves; ++w) qv[w] = qrow[tok[w]];
                     }
                     uint64_t best = 0;
 #pragma unroll
@@ -1505,22 +1672,31 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         const int kd = a.k;
         const bool bonus = (j >= L - 1) || (j >= kd);
         int acc = 0;
+        // candidate rows of q: a hash of this draft row's tokens in LDS (the race below and the accept test look
+        // up q there), or a scan of the row when it has too many candidates for the hash
+        const bool sparse = a.q_ids != nullptr;
+        const bool hashed = sparse && !bonus && a.q_cand <= kQHash / 2;
+        if (hashed) build_q_hash(a, b * kd + j, sh);
+        auto q_at = [&](int64_t i) -> float {
+            if (!sparse) return a.q[(b * kd + j) * a.vocab + i];
+            return hashed ? q_hash_lookup(sh, i) : sparse_q_scan(a, b * kd + j, i);
+        };
         if (threadIdx.x == 0 && dec_valid) {
             const float sd = scale_logit(dec_x, temp, unit_temp);
             const float pd = (sel_key(sd) >= theta_key && sel_key(sd) != 0u) ? expf(sd - mu) / rs.z : 0.f;
-            acc = (dec_u * dec_q < pd) ? 1 : 0;
+            const float dq = sparse ? q_at(dec_d) : dec_q;
+            acc = (dec_u * dq < pd) ? 1 : 0;
         }
         uint64_t best = 0;
         if (!rs.dense) {
             const int n = min(sh.count, kCap);
-            const float* qrow = a.q + (b * kd + (bonus ? 0 : j)) * a.vocab;
             const float* erow = a.noise + b * a.vocab;
             for (int c = threadIdx.x; c < n; c += blockDim.x) {
                 const uint32_t key = sh.ckey[c];
                 if (key < theta_key) continue;
                 const int64_t i = sh.cidx[c];
                 const float p = expf(nvs::key_float(key) - mu) / rs.z;
-                const float w = bonus ? p : fmaxf(p - qrow[i], 0.f);
+                const float w = bonus ? p : fmaxf(p - q_at(i), 0.f);
                 const float score = w / erow[i];
                 const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
                                      static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
@@ -2054,13 +2230,14 @@ extern "C" int nvs_spec_accept_workspace_size(int64_t batch, int num_drafts, int
     return NVS_OK;
 }
 
-extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_stride,
-                               const float* temperatures, const int64_t* top_k, const float* top_p, int max_top_k,
-                               int has_top_p, const float* q, const int64_t* drafts, const int64_t* verified_lens,
-                               const float* uniforms, const float* noise, int64_t batch, int num_drafts,
-                               int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail,
-                               int32_t* row_counters, void* workspace, size_t workspace_bytes, void* stream) {
-    nvs::clear_error();
+// The fused accept behind both entry points: q dense (q) or as candidate rows (q_ids / q_probs).
+static int spec_accept_impl(const void* logits, int logits_dtype, int64_t logits_row_stride,
+                            const float* temperatures, const int64_t* top_k, const float* top_p, int max_top_k,
+                            int has_top_p, const float* q, const int32_t* q_ids, const float* q_probs, int q_cand,
+                            int64_t q_stride, const int64_t* drafts, const int64_t* verified_lens,
+                            const float* uniforms, const float* noise, int64_t batch, int num_drafts, int64_t n_pos,
+                            int64_t vocab, int64_t* n_accept, int64_t* tail, int32_t* row_counters, void* workspace,
+                            size_t workspace_bytes, void* stream) {
     int st = check_dtype(logits_dtype);
     if (st != NVS_OK) return st;
     st = accept_common_checks(drafts, batch, num_drafts, n_pos, vocab, n_accept, tail);
@@ -2068,7 +2245,8 @@ extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t log
     st = common_select_checks(logits, logits_row_stride, n_pos, vocab, 1, max_top_k, top_k);
     if (st != NVS_OK) return st;
     if (batch == 0) return NVS_OK;
-    NVS_CHECK(temperatures && q && uniforms && noise && row_counters, NVS_ERR_INVALID, "spec_accept: null pointer");
+    NVS_CHECK(temperatures && (q || (q_ids && q_probs)) && uniforms && noise && row_counters, NVS_ERR_INVALID,
+              "spec_accept: null pointer");
     NVS_CHECK(!has_top_p || top_p != nullptr, NVS_ERR_INVALID, "spec_accept: has_top_p needs top_p");
     NVS_CHECK(verified_lens != nullptr || n_pos == batch * (num_drafts + 1), NVS_ERR_INVALID,
               "spec_accept: logits have %lld positions, expected batch*(k+1) = %lld", (long long)n_pos,
@@ -2088,6 +2266,10 @@ extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t log
     a.has_top_p = has_top_p && max_top_k > 0;
     a.pos_per_param = 1;
     a.q = q;
+    a.q_ids = q_ids;
+    a.q_probs = q_probs;
+    a.q_cand = q_cand;
+    a.q_stride = q_stride;
     a.drafts = drafts;
     a.lens = verified_lens;
     a.uniforms = uniforms;
@@ -2099,4 +2281,39 @@ extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t log
     a.n_accept = n_accept;
     a.tail = tail;
     return launch_select<kModeAccept>(logits_dtype, a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_stride,
+                               const float* temperatures, const int64_t* top_k, const float* top_p, int max_top_k,
+                               int has_top_p, const float* q, const int64_t* drafts, const int64_t* verified_lens,
+                               const float* uniforms, const float* noise, int64_t batch, int num_drafts,
+                               int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail,
+                               int32_t* row_counters, void* workspace, size_t workspace_bytes, void* stream) {
+    nvs::clear_error();
+    NVS_CHECK(q != nullptr || batch == 0, NVS_ERR_INVALID, "spec_accept: q is NULL");
+    return spec_accept_impl(logits, logits_dtype, logits_row_stride, temperatures, top_k, top_p, max_top_k,
+                            has_top_p, q, nullptr, nullptr, 0, 0, drafts, verified_lens, uniforms, noise, batch,
+                            num_drafts, n_pos, vocab, n_accept, tail, row_counters, workspace, workspace_bytes,
+                            stream);
+}
+
+extern "C" int nvs_spec_accept_candidates(const void* logits, int logits_dtype, int64_t logits_row_stride,
+                                          const float* temperatures, const int64_t* top_k, const float* top_p,
+                                          int max_top_k, int has_top_p, const int32_t* cand_ids,
+                                          const float* cand_probs, int num_candidates, int64_t cand_row_stride,
+                                          const int64_t* drafts, const int64_t* verified_lens, const float* uniforms,
+                                          const float* noise, int64_t batch, int num_drafts, int64_t n_pos,
+                                          int64_t vocab, int64_t* n_accept, int64_t* tail, int32_t* row_counters,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+    nvs::clear_error();
+    NVS_CHECK(batch == 0 || (cand_ids != nullptr && cand_probs != nullptr), NVS_ERR_INVALID,
+              "spec_accept_candidates: null candidate rows");
+    NVS_CHECK(num_candidates >= 1 && cand_row_stride >= num_candidates, NVS_ERR_INVALID,
+              "spec_accept_candidates: num_candidates %d with row stride %lld", num_candidates,
+              (long long)cand_row_stride);
+    NVS_CHECK(max_top_k >= 1, NVS_ERR_INVALID, "spec_accept_candidates: candidate rows need top-k (max_top_k >= 1)");
+    return spec_accept_impl(logits, logits_dtype, logits_row_stride, temperatures, top_k, top_p, max_top_k,
+                            has_top_p, nullptr, cand_ids, cand_probs, num_candidates, cand_row_stride, drafts,
+                            verified_lens, uniforms, noise, batch, num_drafts, n_pos, vocab, n_accept, tail,
+                            row_counters, workspace, workspace_bytes, stream);
 }

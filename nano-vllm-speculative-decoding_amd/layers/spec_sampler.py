@@ -257,16 +257,23 @@ def _accept_greedy(logits, drafts, verified_lens):
     return n_accept, tail
 
 
+def _q_tensor(draft_probs):
+    """The tensor to device-check for q: the dense q itself, or the ids of candidate rows."""
+    return draft_probs.ids if hasattr(draft_probs, "ids") else draft_probs
+
+
 def accept_from_logits(target_logits: torch.Tensor, draft_probs: torch.Tensor, drafts: torch.Tensor,
                        sampling: SamplingTensors, verified_lens: torch.Tensor | None,
                        generator: torch.Generator | None) -> tuple[torch.Tensor, torch.Tensor]:
     """What SpeculativeDecoder._accept computes for a random batch (speculative.py:450-462), fused:
         accept_random(probs_from_logits(logits, sampling), q, drafts, g)                       (verified_lens None)
         accept_random_varlen(probs_from_logits(logits, sampling_per_token(...)), q, drafts, lens, g)
-    target_logits: [B, k+1, V] or [T, V]; sampling holds per-row [B] parameters. Draws the same random numbers
-    in the same order and returns the same (n_accept, tail)."""
+    target_logits: [B, k+1, V] or [T, V]; sampling holds per-row [B] parameters. draft_probs: the dense
+    [B, k, V] q, or DSpark's candidate rows (an object with ids [B, k, C] int32 and probs [B, k, C], as
+    layers.markov.CandidateRows), which stand for the q they scatter to. Draws the same random numbers in the
+    same order and returns the same (n_accept, tail)."""
     assert sampling.temperatures is not None, "greedy batches use accept_greedy(_varlen)"
-    _lib.require_device(target_logits, draft_probs, drafts, verified_lens, sampling.temperatures)
+    _lib.require_device(target_logits, _q_tensor(draft_probs), drafts, verified_lens, sampling.temperatures)
     batch_size, num_drafts = drafts.shape
     uniforms, noise = _draws(batch_size, num_drafts, target_logits.shape[-1], target_logits.device, generator)
     return spec_accept_with_draws(target_logits, draft_probs, drafts, sampling, verified_lens, uniforms, noise)
@@ -279,11 +286,20 @@ def spec_accept_with_draws(target_logits: torch.Tensor, draft_probs: torch.Tenso
     """accept_from_logits with the uniforms [B, k] and noise [B, V] supplied by the caller (tests, benchmarks,
     a caller that draws them elsewhere). workspace: optional uint8 scratch buffer for the per-position records.
     The per-row counters live in a persistent zero-filled buffer that every call leaves zero."""
-    _lib.require_device(target_logits, draft_probs, drafts, verified_lens, uniforms, noise)
+    _lib.require_device(target_logits, _q_tensor(draft_probs), drafts, verified_lens, uniforms, noise)
     batch_size, num_drafts = drafts.shape
     rows, n_pos, row_stride = _rows_view(target_logits)
     vocab = target_logits.shape[-1]
-    q = _contig(draft_probs, torch.float32)
+    candidates = hasattr(draft_probs, "ids")
+    if candidates:
+        cand_ids = _contig(draft_probs.ids, torch.int32)
+        cand_probs = _contig(draft_probs.probs, torch.float32)
+        if cand_ids.shape[:2] != (batch_size, num_drafts) or cand_probs.shape != cand_ids.shape:
+            raise ValueError(f"candidate rows {tuple(cand_ids.shape)} / {tuple(cand_probs.shape)} are not [B, k, C]")
+        if not sampling.all_top_k or sampling.max_top_k <= 0:
+            raise ValueError("candidate rows need every row to truncate with top-k (sampling.all_top_k)")
+    else:
+        q = _contig(draft_probs, torch.float32)
     drafts_c = _contig(drafts, torch.int64)
     lens = _contig(verified_lens, torch.int64)
     temps = _contig(sampling.temperatures, torch.float32)
@@ -300,10 +316,19 @@ def spec_accept_with_draws(target_logits: torch.Tensor, draft_probs: torch.Tenso
     _lib.check(lib.nvs_spec_accept_workspace_size(batch_size, num_drafts, n_pos, vocab, sampling.max_top_k,
                                                   ctypes.byref(nbytes)),
                "spec_accept_workspace_size")
-    assert q.shape == (batch_size, num_drafts, vocab), f"draft_probs {tuple(q.shape)} is not [B, k, V]"
     if workspace is None or workspace.numel() < nbytes.value:
         workspace = _lib.workspace(max(nbytes.value, 1), target_logits.device)
     counters = _lib.persistent_workspace("spec_accept_row_counters", 4 * batch_size, target_logits.device)
+    if candidates:
+        _lib.check(lib.nvs_spec_accept_candidates(
+            rows.data_ptr(), _lib.dtype_code(rows.dtype), row_stride, temps.data_ptr(), top_k.data_ptr(),
+            top_p.data_ptr(), sampling.max_top_k, int(sampling.has_top_p), cand_ids.data_ptr(), cand_probs.data_ptr(),
+            cand_ids.shape[-1], cand_ids.shape[-1], drafts_c.data_ptr(), _lib.ptr(lens), u.data_ptr(), e.data_ptr(),
+            batch_size, num_drafts, n_pos, vocab, n_accept.data_ptr(), tail.data_ptr(), counters.data_ptr(),
+            workspace.data_ptr(), workspace.numel(), _lib.stream_of(target_logits)),
+            "spec_accept_candidates")
+        return n_accept, tail
+    assert q.shape == (batch_size, num_drafts, vocab), f"draft_probs {tuple(q.shape)} is not [B, k, V]"
     _lib.check(lib.nvs_spec_accept(rows.data_ptr(), _lib.dtype_code(rows.dtype), row_stride, temps.data_ptr(),
                                    top_k.data_ptr(), top_p.data_ptr(), sampling.max_top_k, int(sampling.has_top_p),
                                    q.data_ptr(), drafts_c.data_ptr(), _lib.ptr(lens), u.data_ptr(), e.data_ptr(),

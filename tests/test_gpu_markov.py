@@ -138,3 +138,49 @@ def test_markov_draw_rejects_bad_arguments(device):
         nm.markov_draw(lg, st, 84, noise, ids.long(), probs, draws)
     with pytest.raises(ValueError):
         nm.markov_draw(lg, sampling(device, None, [20], [1.0]), 84, noise, ids, probs, draws)
+
+
+@pytest.mark.parametrize("top_k, top_p, varlen, dtype", [
+    (20, 1.0, False, torch.float32),      # the wave-0 finish
+    (20, 0.8, True, torch.bfloat16),
+    (100, 0.9, True, torch.float32),     # top-p with rank > 64: the workgroup finish, candidate hash in LDS
+    (600, 1.0, False, torch.float32),    # 664 candidates: more than the hash holds, the row is scanned
+])
+def test_accept_on_candidate_rows_equals_the_dense_q(device, top_k, top_p, varlen, dtype):
+    """A DSpark round: drafts and candidate rows from sample_markov, then the fused accept on the candidate rows
+    and on the q they scatter to, with the same uniforms and noise: the same (n_accept, tail) bit for bit, and
+    the oracle's accept on the dense q agrees."""
+    log_case(f"accept on candidate rows: top_k={top_k} top_p={top_p} varlen={varlen} {dtype}")
+    batch, k, vocab = 16, 7, 32000
+    g = torch.Generator().manual_seed(top_k)
+    target = torch.randn(batch, k + 1, vocab, generator=g) * 3
+    draft_logits = target[:, :k] + torch.randn(batch, k, vocab, generator=g)
+    table = torch.randn(16, vocab, generator=g) * 0.5
+    st = sampling(device, [1.0, 0.8] * (batch // 2), [top_k] * batch, [top_p] * batch)
+    gen = torch.Generator(device=device).manual_seed(9)
+    tab = table.to(device)
+    drafts, rows = nm.sample_markov(draft_logits.to(device), torch.arange(batch, device=device), st,
+                                    lambda prev: tab[prev % 16], gen)
+    assert isinstance(rows, nm.CandidateRows)
+    lens = torch.randint(1, k + 2, (batch,), generator=g) if varlen else None
+    logits = torch.cat([target[b, :int(lens[b])] for b in range(batch)]) if varlen else target.reshape(-1, vocab)
+    lg = logits.to(dtype).to(device)
+    uniforms = torch.rand(batch, k, generator=g).to(device)
+    noise = ss.exponential_noise((batch, vocab), g).to(device)
+    lens_d = None if lens is None else lens.to(device)
+    dense = rows.to_dense(vocab)
+    n_d, t_d = ns.spec_accept_with_draws(lg, dense, drafts, st, lens_d, uniforms, noise)
+    n_s, t_s = ns.spec_accept_with_draws(lg, rows, drafts, st, lens_d, uniforms, noise)
+    torch.cuda.synchronize()
+    assert torch.equal(n_s, n_d) and torch.equal(t_s, t_d), "candidate rows and dense q disagree"
+    cpu = st.temperatures.cpu()
+    per_pos = cpu.repeat_interleave(lens if varlen else torch.full((batch,), k + 1))
+    tk = st.top_k.cpu().repeat_interleave(lens if varlen else torch.full((batch,), k + 1))
+    tp = st.top_p.cpu().repeat_interleave(lens if varlen else torch.full((batch,), k + 1))
+    p = ss.probs_from_logits(lg.cpu(), per_pos, tk, tp, st.max_top_k, st.has_top_p)
+    if varlen:
+        want = ss.accept_random_varlen(p, dense.cpu(), drafts.cpu(), lens, uniforms.cpu(), noise.cpu())
+    else:
+        want = ss.accept_random(p.view(batch, k + 1, vocab), dense.cpu(), drafts.cpu(), uniforms.cpu(), noise.cpu())
+    assert torch.equal(n_s.cpu(), want[0]) and torch.equal(t_s.cpu(), want[1]), "the oracle disagrees"
+    print(f"mean accepted {float(n_s.float().mean()):.2f}")
