@@ -287,6 +287,82 @@ def qk_rope_bench(args, dev):
             "timing": "HIP graph of 20 calls, per call", "kernel": "qk_norm_rope_store_kernel (one launch)"}
 
 
+def markov_bench(args, dev):
+    """DSpark's propose sampling (the draft side of a round): 7 Markov rows at batch 64 over V = 151,936 bf16
+    draft logits, top-k 20 (84 candidates), temperature 1. Each row adds the Markov bias of the token drawn
+    before it: a rank-64 head, embedding gather + GEMM, computed by torch in both versions. Ours: one
+    nvs_markov_draw per row writing candidate rows. Against the same rows as the reference's torch ops
+    (speculative.py:163-184): topk, the truncated softmax, the race, and the scatter into a zeroed [64, 7, V]
+    fp32 q."""
+    import torch
+    import torch.nn.functional as F
+
+    from nvs_amd.layers import markov as nm
+    from nvs_amd.layers import spec_sampler as ns
+
+    B, k, V, r, top_k = 64, 7, 151936, 64, 20
+    g = torch.Generator(device=dev).manual_seed(21)
+    logits = torch.randn(B, k, V, device=dev, generator=g).mul_(3.0).to(torch.bfloat16)
+    w1 = torch.randn(V, r, device=dev, generator=g, dtype=torch.bfloat16).mul_(0.1)
+    w2 = torch.randn(V, r, device=dev, generator=g, dtype=torch.bfloat16).mul_(0.1)
+    anchors = torch.randint(0, V, (B,), device=dev, generator=g)
+    st = ns.SamplingTensors(torch.ones(B, device=dev), torch.full((B,), top_k, dtype=torch.int64, device=dev),
+                            torch.ones(B, device=dev), top_k, False, True)
+    C = nm.num_candidates(top_k, True, V)
+
+    def bias(prev):
+        return F.linear(F.embedding(prev, w1), w2)
+
+    gen = torch.Generator(device=dev).manual_seed(22)
+
+    def ours():
+        return nm.sample_markov(logits, anchors, st, bias, gen)
+
+    q_dense = torch.empty(B, k, V, device=dev)
+    drafts_t = torch.empty(B, k, dtype=torch.int64, device=dev)
+
+    def torch_rows():
+        noise = torch.empty(B, k, C, device=dev).exponential_(1.0, generator=gen).clamp_min_(1e-10)
+        q_dense.zero_()
+        prev = anchors
+        for row in range(k):
+            values, ids = (logits[:, row] + bias(prev)).topk(C, dim=-1)
+            s = values.float()
+            kth = s[:, top_k - 1:top_k]
+            probs = torch.softmax(s.masked_fill(s < kth, float("-inf")), dim=-1)
+            prev = ids.gather(-1, (probs / noise[:, row]).argmax(-1, keepdim=True)).squeeze(-1)
+            q_dense[:, row].scatter_(-1, ids, probs)
+            drafts_t[:, row] = prev
+
+    # one row of our draw alone, on the first row's biased logits
+    row0 = (logits[:, 0] + bias(anchors)).contiguous()
+    noise0 = torch.empty(B, C, device=dev).exponential_(1.0, generator=gen)
+    ids0 = torch.empty(B, C, dtype=torch.int32, device=dev)
+    probs0 = torch.empty(B, C, device=dev)
+    draws0 = torch.empty(B, dtype=torch.int64, device=dev)
+
+    def draw_only():
+        nm.markov_draw(row0, st, C, noise0, ids0, probs0, draws0)
+
+    def bias_only():
+        logits[:, 0] + bias(anchors)
+
+    steps, warm = max(10, args.steps // 4), max(3, args.warmup // 4)
+    ms = time_gpu(ours, steps, warm)
+    ms_t = time_gpu(torch_rows, steps, warm)
+    ms_d = time_gpu(draw_only, steps, warm)
+    ms_b = time_gpu(bias_only, steps, warm)
+    alg = B * V * 2            # one read of a row's bf16 logits per draw
+    log(f"[bench] DSpark propose sampling (7 Markov rows, B 64, V 151936 bf16, 84 candidates): {ms * 1e3:.1f} us "
+        f"vs {ms_t * 1e3:.1f} us as torch ops with dense q; one draw {ms_d * 1e3:.2f} us "
+        f"({alg / (ms_d * 1e-3) / 1e9:.0f} GB/s), bias + add {ms_b * 1e3:.2f} us")
+    return {"workload": "markov_rows_b64_k7_v151936_bf16_topk20_rank64", "us": round(ms * 1e3, 2),
+            "torch_ops_dense_q_us": round(ms_t * 1e3, 2), "draw_us": round(ms_d * 1e3, 2),
+            "draw_GBs": round(alg / (ms_d * 1e-3) / 1e9, 1), "bias_and_add_us": round(ms_b * 1e3, 2),
+            "candidates": C, "q_bytes_dense": B * k * V * 4, "q_bytes_candidates": B * k * C * 8,
+            "kernel": "select_kernel<bf16, markov> (one launch per Markov row)"}
+
+
 def verify_round_bench(args, dev):
     """A whole verify round (the round-level workload): 36 Qwen3-8B-shaped layers over the batch-64 verify batch
     (the attention workload's rows, one forward captured as a HIP graph on the reference's (row slots, tokens)
@@ -422,6 +498,7 @@ def main():
              "qk_norm_rope_store": qk_rope_bench(args, dev)}
     if args.sampler == "on":
         extra["sampler"] = sampler_bench(args, dev)
+        extra["markov_rows"] = markov_bench(args, dev)
     if args.verify_round == "on":
         extra["verify_round"] = verify_round_bench(args, dev)
     if args.copy_probe == "on":

@@ -1001,11 +1001,47 @@ __device__ int64_t nth_tie_end(const SelArgs& a, const char* row, float temp, bo
 // probabilities exp(s - m) / Z with Z over the candidates; the race argmax_c p_c / noise[c] by candidate rank, the
 // first rank on ties, rank 0 when every score is zero; the drawn token and the sparse row (ids, probs), with
 // id -1 and probability 0 past the candidates.
+// Where the kept values are when the tail starts: the wave-0 finish's short list (sortbuf: keys, then indices at
+// 512), the lanes' lists (ckey / cidx, sh.count entries), or only in the row (after the exact path).
+enum KeptSource { kKeptInRow = 0, kKeptInShortList = 1, kKeptInLists = 2 };
+
 template <int DT, bool VEC>
 __device__ void markov_tail(const SelArgs& a, int64_t t, const char* row, float temp, bool unit_temp,
-                            uint32_t theta_key, SelShared& sh) {
+                            uint32_t theta_key, int source, SelShared& sh) {
     uint64_t* pairs = pair_buf(sh);
     const int C = a.n_cand;
+    // The lists hold every value at or above the row's threshold, so the kept ones come from there without a
+    // second pass over the row. Each thread takes its entries into registers before the pairs overwrite them.
+    auto collect_from_lists = [&]() {
+        constexpr int kPer = kCap / kSelThreads;
+        uint32_t kk[kPer];
+        uint32_t ii[kPer];
+        const int n = source == kKeptInShortList ? sh.count : min(sh.count, kCap);
+#pragma unroll
+        for (int s = 0; s < kPer; ++s) {
+            const int c = static_cast<int>(threadIdx.x) + s * kSelThreads;
+            const bool in = c < n && (source == kKeptInLists || s == 0);
+            kk[s] = in ? (source == kKeptInShortList ? sh.sortbuf[c] : sh.ckey[c]) : 0u;
+            ii[s] = in ? (source == kKeptInShortList ? sh.sortbuf[kSelWaves * 64 + c]
+                                                     : static_cast<uint32_t>(sh.cidx[c]))
+                       : 0u;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            sh.count = 0;
+            sh.bin_count = 0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < kPer; ++s) {
+            const uint32_t key = kk[s];
+            if (key == 0u || key < theta_key) continue;
+            const int p = atomicAdd(&sh.count, 1);
+            if (key > theta_key) atomicAdd(&sh.bin_count, 1);
+            pairs[p] = (static_cast<uint64_t>(key) << 32) | (0xffffffffu - ii[s]);
+        }
+        __syncthreads();
+    };
     auto collect = [&](int64_t tie_end) {
         if (threadIdx.x == 0) {
             sh.count = 0;
@@ -1028,7 +1064,11 @@ __device__ void markov_tail(const SelArgs& a, int64_t t, const char* row, float 
         }
         __syncthreads();
     };
-    collect(a.vocab);
+    if (source == kKeptInRow) {
+        collect(a.vocab);
+    } else {
+        collect_from_lists();
+    }
     int n = sh.count;
     if (n > kPairCap) {
         // Only ties at theta make that many: the values above it are fewer than the rank. The candidates are
@@ -1133,6 +1173,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
     rs.dense = !truncating;
     rs.theta = -INFINITY;
     bool record_done = false;   // the wave-0 epilogue already wrote this position's record
+    int kept_source = kKeptInRow;   // where a Markov draw finds the kept values
     if (!truncating) {
         load_decision();
         // online max / sum-exp over the whole row
@@ -1571,6 +1612,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             rs.theta = sh.fast_theta;
             rs.dense = false;
             record_done = true;
+            kept_source = kKeptInShortList;
         } else {
         if (!exact) {
             // the lanes' lists, one after another (wave by wave, lane by lane), at the front of the buffer
@@ -1601,6 +1643,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         if (exact) {
             rs = exact_row_stats<DT, VEC>(a, row, temp, unit_temp, rank, K, top_p, sh);
         } else {
+            kept_source = kKeptInLists;
             const int n = sh.count;
             auto each = [&](auto&& fn) {
                 for (int c = threadIdx.x; c < n; c += blockDim.x) fn(sh.ckey[c]);
@@ -1640,7 +1683,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
     const float mu = (rs.m == -INFINITY) ? 0.f : rs.m;
 
     if constexpr (MODE == kModeMarkov) {
-        markov_tail<DT, VEC>(a, t, row, temp, unit_temp, theta_key, sh);
+        markov_tail<DT, VEC>(a, t, row, temp, unit_temp, theta_key, kept_source, sh);
         return;
     } else if constexpr (MODE == kModeProbs || MODE == kModeTruncate) {
         float* orow = a.out + t * a.out_stride;
