@@ -30,8 +30,9 @@ METRIC = "verify-attn µs/layer & HBM GB/s (% of 8 TB/s) at B=64, 8 q, 3k ctx"
 # by what the counter reads for the 1 GiB copy probe (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); the runs and their
 # numbers are in profiles/hbm_traffic_pmc_verify_attention_and_spec_accept.md. Re-measure after a kernel change.
 MEASURED_TRAFFIC = {
-    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200": 789_786_632,
-    "spec_accept_b64_k7_v151936_fp32_topk64": 320_000_031,
+    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200": 789_784_400,
+    "spec_accept_b64_k7_v151936_fp32_topk64": 320_062_639,
+    "markov_draw_b64_v151936_bf16_topk20": 20_145_685,
 }
 
 
@@ -360,6 +361,7 @@ def markov_bench(args, dev):
             "torch_ops_dense_q_us": round(ms_t * 1e3, 2), "draw_us": round(ms_d * 1e3, 2),
             "draw_GBs": round(alg / (ms_d * 1e-3) / 1e9, 1), "bias_and_add_us": round(ms_b * 1e3, 2),
             "candidates": C, "q_bytes_dense": B * k * V * 4, "q_bytes_candidates": B * k * C * 8,
+            "draw_traffic": MEASURED_TRAFFIC["markov_draw_b64_v151936_bf16_topk20"], "draw_algorithmic_bytes": alg,
             "kernel": "select_kernel<bf16, markov> (one launch per Markov row)"}
 
 
