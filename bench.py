@@ -32,7 +32,6 @@ METRIC = "verify-attn µs/layer & HBM GB/s (% of 8 TB/s) at B=64, 8 q, 3k ctx"
 MEASURED_TRAFFIC = {
     "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200": 789_784_400,
     "spec_accept_b64_k7_v151936_fp32_topk64": 320_062_639,
-    "markov_draw_b64_v151936_bf16_topk20": 20_145_685,
 }
 
 
@@ -291,10 +290,11 @@ def qk_rope_bench(args, dev):
 def markov_bench(args, dev):
     """DSpark's propose sampling (the draft side of a round): 7 Markov rows at batch 64 over V = 151,936 bf16
     draft logits, top-k 20 (84 candidates), temperature 1. Each row adds the Markov bias of the token drawn
-    before it: a rank-64 head, embedding gather + GEMM, computed by torch in both versions. Ours: one
-    nvs_markov_draw per row writing candidate rows. Against the same rows as the reference's torch ops
-    (speculative.py:163-184): topk, the truncated softmax, the race, and the scatter into a zeroed [64, 7, V]
-    fp32 q."""
+    before it: a rank-64 head, embedding gather + GEMM by torch in both versions. Ours: one nvs_markov_draw per
+    row, the bias added inside it, writing candidate rows. Against the same rows as the reference's torch ops
+    (speculative.py:163-184): the add, topk, the truncated softmax, the race, and the scatter into a zeroed
+    [64, 7, V] fp32 q. Both are captured as HIP graphs and replayed, as the reference replays its sampling graphs,
+    with the noise drawn outside them."""
     import torch
     import torch.nn.functional as F
 
@@ -310,20 +310,20 @@ def markov_bench(args, dev):
     st = ns.SamplingTensors(torch.ones(B, device=dev), torch.full((B,), top_k, dtype=torch.int64, device=dev),
                             torch.ones(B, device=dev), top_k, False, True)
     C = nm.num_candidates(top_k, True, V)
+    noise = torch.empty(B, k, C, device=dev).exponential_(1.0, generator=g).clamp_min_(1e-10)
 
     def bias(prev):
         return F.linear(F.embedding(prev, w1), w2)
 
-    gen = torch.Generator(device=dev).manual_seed(22)
+    drafts = torch.empty(B, k, dtype=torch.int64, device=dev)
 
     def ours():
-        return nm.sample_markov(logits, anchors, st, bias, gen)
+        nm.markov_rows(logits, anchors, st, bias, noise, drafts, C)
 
     q_dense = torch.empty(B, k, V, device=dev)
     drafts_t = torch.empty(B, k, dtype=torch.int64, device=dev)
 
     def torch_rows():
-        noise = torch.empty(B, k, C, device=dev).exponential_(1.0, generator=gen).clamp_min_(1e-10)
         q_dense.zero_()
         prev = anchors
         for row in range(k):
@@ -335,34 +335,42 @@ def markov_bench(args, dev):
             q_dense[:, row].scatter_(-1, ids, probs)
             drafts_t[:, row] = prev
 
-    # one row of our draw alone, on the first row's biased logits
-    row0 = (logits[:, 0] + bias(anchors)).contiguous()
-    noise0 = torch.empty(B, C, device=dev).exponential_(1.0, generator=gen)
+    # one row of our draw alone (bias given, added inside), and the torch bias alone
+    b0 = bias(anchors)
     ids0 = torch.empty(B, C, dtype=torch.int32, device=dev)
     probs0 = torch.empty(B, C, device=dev)
     draws0 = torch.empty(B, dtype=torch.int64, device=dev)
 
     def draw_only():
-        nm.markov_draw(row0, st, C, noise0, ids0, probs0, draws0)
+        nm.markov_draw(logits[:, 0], st, C, noise[:, 0], ids0, probs0, draws0, bias=b0)
 
     def bias_only():
-        logits[:, 0] + bias(anchors)
+        bias(anchors)
+
+    def graphed(fn):
+        fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        return graph.replay
 
     steps, warm = max(10, args.steps // 4), max(3, args.warmup // 4)
-    ms = time_gpu(ours, steps, warm)
-    ms_t = time_gpu(torch_rows, steps, warm)
-    ms_d = time_gpu(draw_only, steps, warm)
-    ms_b = time_gpu(bias_only, steps, warm)
-    alg = B * V * 2            # one read of a row's bf16 logits per draw
-    log(f"[bench] DSpark propose sampling (7 Markov rows, B 64, V 151936 bf16, 84 candidates): {ms * 1e3:.1f} us "
-        f"vs {ms_t * 1e3:.1f} us as torch ops with dense q; one draw {ms_d * 1e3:.2f} us "
-        f"({alg / (ms_d * 1e-3) / 1e9:.0f} GB/s), bias + add {ms_b * 1e3:.2f} us")
+    ms = time_gpu(graphed(ours), steps, warm)
+    ms_t = time_gpu(graphed(torch_rows), steps, warm)
+    ms_d = time_gpu(graphed(draw_only), steps, warm)
+    ms_b = time_gpu(graphed(bias_only), steps, warm)
+    same = bool(torch.equal(drafts, drafts_t))
+    alg = 2 * B * V * 2        # one read of a row's bf16 logits and of its bf16 bias per draw
+    log(f"[bench] DSpark propose sampling (7 Markov rows, B 64, V 151936 bf16, 84 candidates, HIP graphs): "
+        f"{ms * 1e3:.1f} us vs {ms_t * 1e3:.1f} us as torch ops with dense q (same drafts: {same}); one draw "
+        f"{ms_d * 1e3:.2f} us ({alg / (ms_d * 1e-3) / 1e9:.0f} GB/s with its bias), Markov head GEMM {ms_b * 1e3:.2f} us")
     return {"workload": "markov_rows_b64_k7_v151936_bf16_topk20_rank64", "us": round(ms * 1e3, 2),
-            "torch_ops_dense_q_us": round(ms_t * 1e3, 2), "draw_us": round(ms_d * 1e3, 2),
-            "draw_GBs": round(alg / (ms_d * 1e-3) / 1e9, 1), "bias_and_add_us": round(ms_b * 1e3, 2),
+            "torch_ops_dense_q_us": round(ms_t * 1e3, 2), "same_drafts": same, "draw_us": round(ms_d * 1e3, 2),
+            "draw_GBs": round(alg / (ms_d * 1e-3) / 1e9, 1), "markov_head_gemm_us": round(ms_b * 1e3, 2),
             "candidates": C, "q_bytes_dense": B * k * V * 4, "q_bytes_candidates": B * k * C * 8,
-            "draw_traffic": MEASURED_TRAFFIC["markov_draw_b64_v151936_bf16_topk20"], "draw_algorithmic_bytes": alg,
-            "kernel": "select_kernel<bf16, markov> (one launch per Markov row)"}
+            "draw_algorithmic_bytes": alg,
+            "kernel": "markov_segment_kernel + markov_merge_kernel (one pair per Markov row)"}
 
 
 def verify_round_bench(args, dev):

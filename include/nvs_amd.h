@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NVS_ABI_VERSION 4
+#define NVS_ABI_VERSION 5
 
 typedef enum {
     NVS_OK = 0,
@@ -222,8 +222,9 @@ int nvs_spec_accept_candidates(const void* logits, int logits_dtype, int64_t log
 
 /* ------------------------------------------------------------------------------------------------ Markov draw
  * Replaces one candidate row of DFlashDrafter._markov_rows (nanovllm/engine/speculative.py:163-184, the
- * `elif candidates:` branch): for each of `batch` sequences, given that row's biased draft logits
- * (logits[:, row] + markov_head(prev), computed by the caller as the reference does):
+ * `elif candidates:` branch): for each of `batch` sequences,
+ *   row_logits = dtype(logits[b] + bias[b])                    (bias: the row's Markov bias, markov_head(prev);
+ *                                                               NULL when the caller added it already)
  *   values, ids = topk(row_logits, num_candidates)            (ties in index order)
  *   probs = probs_from_logits(values, sampling)                (temperature, top-k, top-p over the candidates)
  *   token = ids[race(probs, noise[:, row])]                    (argmax of probs / noise, first rank on ties)
@@ -233,16 +234,19 @@ int nvs_spec_accept_candidates(const void* logits, int logits_dtype, int64_t log
  * reference and never win its race unless every probability is 0 (then rank 0, the row's largest value).
  * num_candidates is the reference's num_candidates() = min(max_top_k + 64, vocab); every row must truncate with
  * top-k (the reference's candidate rows require it; a row with top_k <= 0 is drawn among its top max_top_k).
- * logits [batch, vocab] fp32 / bf16 / fp16 with a row stride; noise [batch, >= num_candidates] fp32, the row's
- * exponential noise by candidate rank; parameters per row as in nvs_probs_from_logits. min(max_top_k, vocab) <=
- * num_candidates <= 7168.
- * One launch per row of the draft block; the rows are sequential because each row's bias depends on the token
- * drawn before it. */
-int nvs_markov_draw(const void* logits, int logits_dtype, int64_t logits_row_stride, int64_t batch, int64_t vocab,
-                    const float* temperatures, const int64_t* top_k, const float* top_p, int max_top_k,
-                    int has_top_p, int num_candidates, const float* noise, int64_t noise_row_stride,
-                    int32_t* cand_ids, float* cand_probs, int64_t cand_row_stride, int64_t* draws,
-                    int64_t draws_stride, void* stream);
+ * logits and bias [batch, vocab] fp32 / bf16 / fp16 (one dtype) with row strides; noise [batch, >= num_candidates]
+ * fp32, the row's exponential noise by candidate rank; parameters per row as in nvs_probs_from_logits.
+ * min(max_top_k, vocab) <= num_candidates <= 7168; batch <= 65535. Up to 512 candidates the row is cut into
+ * segments drawn by separate workgroups and merged (workspace: nvs_markov_draw_workspace_size bytes, no
+ * initialisation); above 512 one workgroup draws each row, needs no workspace, and takes no bias (add it first).
+ * The rows of a draft block are sequential launches because each row's bias depends on the token drawn before it. */
+int nvs_markov_draw_workspace_size(int64_t batch, int64_t vocab, int num_candidates, size_t* bytes);
+int nvs_markov_draw(const void* logits, int logits_dtype, int64_t logits_row_stride, const void* bias,
+                    int64_t bias_row_stride, int64_t batch, int64_t vocab, const float* temperatures,
+                    const int64_t* top_k, const float* top_p, int max_top_k, int has_top_p, int num_candidates,
+                    const float* noise, int64_t noise_row_stride, int32_t* cand_ids, float* cand_probs,
+                    int64_t cand_row_stride, int64_t* draws, int64_t draws_stride, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------ decoder-layer elementwise ops
  * The elementwise steps between the projections of a Qwen3 decoder layer, so that a whole verify forward runs

@@ -996,6 +996,40 @@ __device__ int64_t nth_tie_end(const SelArgs& a, const char* row, float temp, bo
     return a.vocab;
 }
 
+// The end of a Markov draw, once the candidates pairs[0..nc) (value descending) are kept: probabilities
+// exp(s - m) / Z with Z over the candidates, the race argmax_c p_c / noise[c] (first rank on ties, rank 0 when every
+// score is zero), the candidate row (id -1 and probability 0 past the candidates) and the drawn token.
+__device__ void markov_emit(const uint64_t* pairs, int nc, int C, const float* noise, int32_t* ids, float* probs,
+                            int64_t* draw, SelShared& sh) {
+    const float m = nc > 0 ? nvs::key_float(static_cast<uint32_t>(pairs[0] >> 32)) : 0.f;
+    float z = 0.f;
+    for (int c = threadIdx.x; c < nc; c += blockDim.x)
+        z += expf(nvs::key_float(static_cast<uint32_t>(pairs[c] >> 32)) - m);
+    z = block_sum(z, sh);
+    uint64_t best = 0;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float p = 0.f;
+        int32_t id = -1;
+        if (c < nc) {
+            const uint64_t pr = pairs[c];
+            p = expf(nvs::key_float(static_cast<uint32_t>(pr >> 32)) - m) / z;
+            id = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(pr));
+        }
+        ids[c] = id;
+        probs[c] = p;
+        const float score = p / noise[c];
+        const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+                             static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(c));
+        best = best > k64 ? best : k64;
+    }
+    best = block_max_u64(best, sh);
+    if (threadIdx.x == 0) {
+        const float score = nvs::key_float(static_cast<uint32_t>(best >> 32));
+        const int win = (score > 0.f) ? static_cast<int>(0xffffffffu - static_cast<uint32_t>(best)) : 0;
+        *draw = win < nc ? static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(pairs[win])) : int64_t{0};
+    }
+}
+
 // DSpark's Markov row (speculative.py:173-180) for one position, after the row statistics: the candidates are
 // the kept values (key >= theta_key) in (value descending, index ascending) order, at most n_cand of them; their
 // probabilities exp(s - m) / Z with Z over the candidates; the race argmax_c p_c / noise[c] by candidate rank, the
@@ -1079,37 +1113,360 @@ __device__ void markov_tail(const SelArgs& a, int64_t t, const char* row, float 
         n = sh.count;
     }
     block_sort_desc_u64(pairs, n);
-    const int nc = min(n, C);
-    const float m = nc > 0 ? nvs::key_float(static_cast<uint32_t>(pairs[0] >> 32)) : 0.f;
-    float z = 0.f;
-    for (int c = threadIdx.x; c < nc; c += blockDim.x) z += expf(nvs::key_float(static_cast<uint32_t>(pairs[c] >> 32)) - m);
-    z = block_sum(z, sh);
-    int32_t* ids = a.cand_ids + t * a.cand_stride;
-    float* probs = a.cand_probs + t * a.cand_stride;
-    const float* noise = a.noise + t * a.noise_stride;
-    uint64_t best = 0;
-    for (int c = threadIdx.x; c < C; c += blockDim.x) {
-        float p = 0.f;
-        int32_t id = -1;
-        if (c < nc) {
-            const uint64_t pr = pairs[c];
-            p = expf(nvs::key_float(static_cast<uint32_t>(pr >> 32)) - m) / z;
-            id = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(pr));
+    markov_emit(pairs, min(n, C), C, a.noise + t * a.noise_stride, a.cand_ids + t * a.cand_stride,
+                a.cand_probs + t * a.cand_stride, a.draws + t * a.draws_stride, sh);
+}
+
+// ---------------------------------------------------------------- Markov draw split over segments of the row
+// With one workgroup per sequence a batch of 64 leaves three quarters of the chip idle, so the split draw cuts each
+// row into segments of at most kSegKeys values, one workgroup each (8 at V = 151,936: 512 workgroups).
+// markov_segment_kernel keeps its segment's keys in registers, 40 per thread (the Markov bias added and rounded to
+// the logits' dtype, the temperature applied), and writes its top n_cand (key, index) pairs in (value descending,
+// index ascending) order of selection: range histograms find the n_cand-th largest key, the values above it are
+// taken, and the ties at it in index order. The row's top n_cand are among the union of its segments' top n_cand, so markov_merge_kernel
+// sorts that union, keeps its first n_cand as the candidates and finishes as markov_tail does: the top-k threshold
+// and the nucleus over the candidates (the same functions as probs_from_logits), Z, the race and the outputs.
+
+constexpr int kSegKeys = 19456;          // values of one segment (at most 40 per thread, kept in registers)
+constexpr int kSplitMaxCand = 512;       // candidates of the split draw (segments x candidates within kPairCap / 2)
+
+struct MarkovSplitArgs {
+    const void* logits;
+    int64_t row_stride;
+    const void* bias;            // [batch, vocab] in the logits' dtype, or null
+    int64_t bias_stride;
+    int64_t batch;
+    int64_t vocab;
+    const float* temps;
+    const int64_t* top_k;
+    const float* top_p;
+    int max_top_k;
+    int has_top_p;
+    int n_cand;
+    int seg_len;                 // a multiple of 8
+    int n_seg;
+    uint64_t* pairs;             // [batch, n_seg, n_cand]
+    const float* noise;
+    int64_t noise_stride;
+    int32_t* cand_ids;
+    float* cand_probs;
+    int64_t cand_stride;
+    int64_t* draws;
+    int64_t draws_stride;
+};
+
+template <int DT>
+__device__ __forceinline__ float round_to_dtype(float x) {
+    if constexpr (DT == NVS_DTYPE_F32) {
+        return x;
+    } else if constexpr (DT == NVS_DTYPE_BF16) {
+        return nvs::bf16_bits_to_float(nvs::float_to_bf16_bits(x));
+    } else {
+        return __half2float(__float2half_rn(x));
+    }
+}
+
+// Element `hi` (0: low half) of a 32-bit word holding two 16-bit values of the dtype.
+template <int DT>
+__device__ __forceinline__ float half_of(uint32_t w, int hi) {
+    const uint16_t bits = static_cast<uint16_t>(hi ? (w >> 16) : (w & 0xffffu));
+    if constexpr (DT == NVS_DTYPE_BF16) {
+        return nvs::bf16_bits_to_float(bits);
+    } else {
+        return nvs::f16_bits_to_float(bits);
+    }
+}
+
+template <int DT, bool VEC, bool BIAS>
+__global__ __launch_bounds__(kSelThreads, 2) void markov_segment_kernel(MarkovSplitArgs a) {
+#pragma clang fp contract(off)
+    __shared__ uint32_t hist[256];
+    __shared__ int n_gt;
+    __shared__ uint32_t pick_bin, pick_rem;
+    __shared__ uint32_t wbound[kSelWaves], whi[kSelWaves];
+    constexpr int W = piece_elems<DT>();
+    const int seg = blockIdx.x;
+    const int64_t b = blockIdx.y;
+    const int64_t e_lo = static_cast<int64_t>(seg) * a.seg_len;
+    const int n = static_cast<int>(min(static_cast<int64_t>(a.seg_len), a.vocab - e_lo));
+    const float temp = a.temps[b];
+    const bool unit_temp = (temp == 1.f);
+    const int es = nvs::dtype_size(DT);
+    const char* row = static_cast<const char*>(a.logits) + (b * a.row_stride + e_lo) * es;
+    const char* brow = BIAS ? static_cast<const char*>(a.bias) + (b * a.bias_stride + e_lo) * es : nullptr;
+    // keys of the segment: s = dtype(logit + bias) / temperature (the reference's row_logits, then
+    // probs_from_logits' division); NaN maps to key 0, below every value
+    const int pieces = (n + W - 1) / W;
+    // every piece of this thread requested before any is used (clamped into the segment, no branch: a load behind
+    // a branch is sunk to its use and the requests would go out one round trip at a time)
+    constexpr int kMaxPc = (kSegKeys / W + kSelThreads - 1) / kSelThreads;
+    __shared__ int tie_part[kMaxPc][kSelWaves];
+    u32x4 raw[kMaxPc];
+    u32x4 braw[BIAS ? kMaxPc : 1];
+#pragma unroll
+    for (int j = 0; j < kMaxPc; ++j) {
+        const int pc = min(static_cast<int>(threadIdx.x) + j * kSelThreads, pieces - 1);
+        if constexpr (VEC) {
+            raw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row) + pc);
+            if constexpr (BIAS) braw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(brow) + pc);
+        } else {
+            // element loads, packed like the 16-byte pieces (clamped indices)
+            uint32_t w4[4] = {0u, 0u, 0u, 0u}, b4[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int c = 0; c < W; ++c) {
+                const int i = min(pc * W + c, n - 1);
+                if constexpr (DT == NVS_DTYPE_F32) {
+                    w4[c] = reinterpret_cast<const uint32_t*>(row)[i];
+                    if constexpr (BIAS) b4[c] = reinterpret_cast<const uint32_t*>(brow)[i];
+                } else {
+                    const uint32_t h = reinterpret_cast<const uint16_t*>(row)[i];
+                    w4[c >> 1] |= (c & 1) ? (h << 16) : h;
+                    if constexpr (BIAS) {
+                        const uint32_t hb = reinterpret_cast<const uint16_t*>(brow)[i];
+                        b4[c >> 1] |= (c & 1) ? (hb << 16) : hb;
+                    }
+                }
+            }
+            raw[j] = u32x4{w4[0], w4[1], w4[2], w4[3]};
+            if constexpr (BIAS) braw[j] = u32x4{b4[0], b4[1], b4[2], b4[3]};
         }
-        ids[c] = id;
-        probs[c] = p;
-        const float score = p / noise[c];
-        const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
-                             static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(c));
-        best = best > k64 ? best : k64;
     }
-    best = block_max_u64(best, sh);
-    if (threadIdx.x == 0) {
-        const float score = nvs::key_float(static_cast<uint32_t>(best >> 32));
-        const int win = (score > 0.f) ? static_cast<int>(0xffffffffu - static_cast<uint32_t>(best)) : 0;
-        a.draws[t * a.draws_stride] =
-            win < nc ? static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(pairs[win])) : int64_t{0};
+    uint32_t tmax = 0u;   // this thread's largest key
+    // The thread's keys stay in registers. Register slot q holds element (threadIdx.x + (q / W) * kSelThreads) *
+    // W + q % W, so index order is (q / W, thread, q % W); the valid slots are a prefix, q < qlim.
+    uint32_t kr[kMaxPc * W];
+    int qlim = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxPc; ++j) {
+        const int pc = static_cast<int>(threadIdx.x) + j * kSelThreads;
+        const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+        float v[W];
+        float bv[W];
+        if constexpr (DT == NVS_DTYPE_F32) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c] = __uint_as_float(w4[c]);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                v[2 * c] = half_of<DT>(w4[c], 0);
+                v[2 * c + 1] = half_of<DT>(w4[c], 1);
+            }
+        }
+        if constexpr (BIAS) {
+            const uint32_t b4[4] = {braw[j].x, braw[j].y, braw[j].z, braw[j].w};
+            if constexpr (DT == NVS_DTYPE_F32) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) bv[c] = __uint_as_float(b4[c]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    bv[2 * c] = half_of<DT>(b4[c], 0);
+                    bv[2 * c + 1] = half_of<DT>(b4[c], 1);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < W; ++c) {
+            const int i = pc * W + c;
+            float x = v[c];
+            if constexpr (BIAS) x = round_to_dtype<DT>(x + bv[c]);
+            const uint32_t key = sel_key(scale_logit(x, temp, unit_temp));
+            kr[j * W + c] = key;
+            if (pc < pieces && i < n) {
+                tmax = max(tmax, key);
+                qlim = j * W + c + 1;
+            }
+        }
     }
+    __syncthreads();
+    // The want-th largest key. A lower bound first: each wave's ceil(want / 8)-th largest lane maximum (one ballot
+    // per bit), the smallest over the waves; every wave has that many lanes holding a key at or above it, so at
+    // least `want` keys are. Then histograms of the keys in [lo, lo + span], 256 bins spread over the range (keys
+    // of logits crowd into a few exponent values, so bins of fixed key digits would collide), each pass narrowing
+    // the range to the bin that holds the wanted rank, until a bin is one key.
+    const int want = min(a.n_cand, n);
+    const int rw = (want + kSelWaves - 1) / kSelWaves;   // <= 64: want <= kSplitMaxCand
+    uint32_t wb = 0u;
+#pragma unroll
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t cand = wb | (1u << bit);
+        if (__popcll(__ballot(tmax >= cand)) >= rw) wb = cand;
+    }
+    const uint32_t wmaxk = wave_max_u32(tmax);
+    if (lane_id() == 0) {
+        wbound[threadIdx.x >> 6] = wb;
+        whi[threadIdx.x >> 6] = wmaxk;
+    }
+    __syncthreads();
+    uint32_t lo = 0xffffffffu, hi = 0u;
+    for (int w = 0; w < kSelWaves; ++w) {
+        lo = min(lo, wbound[w]);
+        hi = max(hi, whi[w]);
+    }
+    uint32_t span = hi - lo;
+    uint32_t rank = static_cast<uint32_t>(want);
+    for (int pass = 0; pass < 5 && want > 0; ++pass) {
+        const int shift = span < 256u ? 0 : 24 - __clz(span);   // (span >> shift) < 256
+        if (threadIdx.x < 256) hist[threadIdx.x] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kMaxPc * W; ++q) {
+            const uint32_t d = kr[q] - lo;   // wraps for keys below lo, which then exceed span
+            if (q < qlim && kr[q] >= lo && d <= span) atomicAdd(&hist[d >> shift], 1u);
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            uint32_t bin, rem;
+            wave_pick_bin(hist, rank, bin, rem);
+            if (threadIdx.x == 0) {
+                pick_bin = bin;
+                pick_rem = rem;
+            }
+        }
+        __syncthreads();
+        lo += pick_bin << shift;
+        rank = pick_rem;
+        if (shift == 0) break;
+        span = (1u << shift) - 1u;
+    }
+    const uint32_t prefix = lo;
+    const uint32_t t_key = prefix;
+    uint64_t* out = a.pairs + (b * a.n_seg + seg) * a.n_cand;
+    // The keys above the threshold (fewer than want) in any order, then the first want - n_gt ties in index
+    // order. Ties of each register group are counted per thread, and one workgroup prefix over all groups at once
+    // gives every tie its rank.
+    if (threadIdx.x == 0) n_gt = 0;
+    int cnt[kMaxPc];
+#pragma unroll
+    for (int j = 0; j < kMaxPc; ++j) {
+        cnt[j] = 0;
+#pragma unroll
+        for (int c = 0; c < W; ++c) cnt[j] += (j * W + c < qlim && want > 0 && kr[j * W + c] == t_key) ? 1 : 0;
+    }
+    int incl[kMaxPc];
+#pragma unroll
+    for (int j = 0; j < kMaxPc; ++j) incl[j] = wave_scan_incl_dpp(cnt[j]);
+    __syncthreads();
+    if (lane_id() == 63) {
+#pragma unroll
+        for (int j = 0; j < kMaxPc; ++j) tie_part[j][threadIdx.x >> 6] = incl[j];
+    }
+#pragma unroll
+    for (int q = 0; q < kMaxPc * W; ++q) {
+        const uint32_t k = kr[q];
+        if (q < qlim && want > 0 && k > t_key) {
+            const int i = (static_cast<int>(threadIdx.x) + (q / W) * kSelThreads) * W + q % W;
+            out[atomicAdd(&n_gt, 1)] = (static_cast<uint64_t>(k) << 32) |
+                                       (0xffffffffu - static_cast<uint32_t>(e_lo + i));
+        }
+    }
+    __syncthreads();
+    const int gt = n_gt;
+    const int need = want - gt;
+    const int wave = static_cast<int>(threadIdx.x >> 6);
+    int base = 0;   // ties of earlier groups, every thread
+#pragma unroll
+    for (int j = 0; j < kMaxPc; ++j) {
+        int before = 0, total_j = 0;
+        for (int w = 0; w < kSelWaves; ++w) {
+            const int c = tie_part[j][w];
+            total_j += c;
+            before += (w < wave) ? c : 0;
+        }
+        int r = base + before + incl[j] - cnt[j];   // rank of this thread's first tie of group j
+#pragma unroll
+        for (int c = 0; c < W; ++c) {
+            const int q = j * W + c;
+            if (q < qlim && want > 0 && kr[q] == t_key) {
+                if (r < need) {
+                    const int i = (static_cast<int>(threadIdx.x) + j * kSelThreads) * W + c;
+                    out[gt + r] = (static_cast<uint64_t>(t_key) << 32) |
+                                  (0xffffffffu - static_cast<uint32_t>(e_lo + i));
+                }
+                ++r;
+            }
+        }
+        base += total_j;
+    }
+    // empty slots (a segment with fewer values than candidates) hold 0, below every pair
+    for (int p = want + threadIdx.x; p < a.n_cand; p += kSelThreads) out[p] = 0ull;
+}
+
+__global__ __launch_bounds__(kSelThreads, 2) void markov_merge_kernel(MarkovSplitArgs a) {
+    __shared__ SelShared sh;
+    const int64_t b = blockIdx.x;
+    uint64_t* pairs = pair_buf(sh);
+    const int total = a.n_seg * a.n_cand;
+    const int C = a.n_cand;
+    // The union of the segments' pairs goes to the upper half of the pair space. Every pair is distinct (one index
+    // each), except the zeros of empty slots. The want-th largest pair is found by a radix select on the keys,
+    // then on the low words of the pairs tied at that key. The pairs at or above it, exactly `want`, go to
+    // [512, 1024), and each is placed at its rank among them in [0, n_cand).
+    const uint64_t* src = a.pairs + b * total;
+    uint64_t* all = pairs + kPairCap / 2;
+    uint64_t* sel = pairs + kSplitMaxCand;
+    int nz = 0;
+    for (int i = threadIdx.x; i < total; i += kSelThreads) {
+        const uint64_t v = src[i];
+        all[i] = v;
+        nz += v != 0ull ? 1 : 0;
+    }
+    for (int i = threadIdx.x; i < C; i += kSelThreads) pairs[i] = 0ull;
+    nz = static_cast<int>(block_sum(static_cast<float>(nz), sh));   // its barriers publish `all`
+    const int want = min(C, nz);
+    if (want > 0) {
+        uint32_t ng, ne;
+        auto each_key = [&](auto&& fn) {
+            for (int i = threadIdx.x; i < total; i += kSelThreads)
+                if (all[i] != 0ull) fn(static_cast<uint32_t>(all[i] >> 32));
+        };
+        const uint32_t t_key = radix_select(each_key, static_cast<uint32_t>(want), sh, &ng, &ne);
+        auto each_low = [&](auto&& fn) {
+            for (int i = threadIdx.x; i < total; i += kSelThreads) {
+                const uint64_t v = all[i];
+                if (v != 0ull && static_cast<uint32_t>(v >> 32) == t_key) fn(static_cast<uint32_t>(v));
+            }
+        };
+        uint32_t ng2, ne2;
+        const uint32_t t_low = radix_select(each_low, static_cast<uint32_t>(want) - ng, sh, &ng2, &ne2);
+        const uint64_t t_pair = (static_cast<uint64_t>(t_key) << 32) | t_low;
+        if (threadIdx.x == 0) sh.count = 0;
+        __syncthreads();
+        for (int i = threadIdx.x; i < total; i += kSelThreads) {
+            const uint64_t v = all[i];
+            if (v != 0ull && v >= t_pair) sel[atomicAdd(&sh.count, 1)] = v;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < want; i += kSelThreads) {
+            const uint64_t v = sel[i];
+            int above = 0;
+            for (int j = 0; j < want; ++j) above += (sel[j] > v) ? 1 : 0;
+            pairs[above] = v;
+        }
+    }
+    __syncthreads();
+    const int real = want;
+    const int K = static_cast<int>(min(static_cast<int64_t>(a.max_top_k), a.vocab));
+    const int64_t tk = a.top_k[b];
+    int rank = static_cast<int>(min(tk > 0 ? tk : static_cast<int64_t>(K), static_cast<int64_t>(K)));
+    rank = min(rank, real);
+    uint32_t theta_key = 0xffffffffu;   // no value: nothing kept
+    if (rank > 0) {
+        const uint32_t thr_key = static_cast<uint32_t>(pairs[rank - 1] >> 32);
+        float theta = nvs::key_float(thr_key);
+        if (a.has_top_p) {
+            for (int i = threadIdx.x; i < rank; i += kSelThreads) sh.sortbuf[i] = static_cast<uint32_t>(pairs[i] >> 32);
+            __syncthreads();
+            theta = top_p_threshold(sh, rank, K, a.top_p[b], theta);
+        }
+        theta_key = nvs::float_key(theta);
+    }
+    // the kept candidates form a prefix of the sorted pairs
+    int kept = 0;
+    for (int c = threadIdx.x; c < real; c += kSelThreads) kept += (static_cast<uint32_t>(pairs[c] >> 32) >= theta_key) ? 1 : 0;
+    kept = static_cast<int>(block_sum(static_cast<float>(kept), sh));
+    markov_emit(pairs, kept, C, a.noise + b * a.noise_stride, a.cand_ids + b * a.cand_stride,
+                a.cand_probs + b * a.cand_stride, a.draws + b * a.draws_stride, sh);
 }
 
 template <int DT, int MODE, bool VEC>
@@ -2078,11 +2435,54 @@ extern "C" int nvs_truncate_logits(const float* scaled, int64_t scaled_row_strid
     return launch_select<kModeTruncate>(NVS_DTYPE_F32, a, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t logits_row_stride, int64_t batch,
-                               int64_t vocab, const float* temperatures, const int64_t* top_k, const float* top_p,
-                               int max_top_k, int has_top_p, int num_candidates, const float* noise,
-                               int64_t noise_row_stride, int32_t* cand_ids, float* cand_probs,
-                               int64_t cand_row_stride, int64_t* draws, int64_t draws_stride, void* stream) {
+// Segments of the split Markov draw for a row of `vocab` values: (segments, values per segment, a multiple of 8).
+static void markov_segments(int64_t vocab, int* n_seg, int* seg_len) {
+    int64_t segs = (vocab + kSegKeys - 1) / kSegKeys;
+    int64_t len = (vocab + segs - 1) / segs;
+    len = (len + 7) / 8 * 8;
+    segs = (vocab + len - 1) / len;
+    *n_seg = static_cast<int>(segs);
+    *seg_len = static_cast<int>(len);
+}
+
+static bool markov_split(int64_t vocab, int num_candidates) {
+    int n_seg, seg_len;
+    markov_segments(vocab, &n_seg, &seg_len);
+    return num_candidates <= kSplitMaxCand && static_cast<int64_t>(n_seg) * num_candidates <= kPairCap / 2;
+}
+
+template <int DT>
+static void launch_markov_split(const MarkovSplitArgs& a, bool vec, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(a.n_seg), static_cast<unsigned>(a.batch));
+    if (vec && a.bias) {
+        hipLaunchKernelGGL((markov_segment_kernel<DT, true, true>), grid, dim3(kSelThreads), 0, s, a);
+    } else if (vec) {
+        hipLaunchKernelGGL((markov_segment_kernel<DT, true, false>), grid, dim3(kSelThreads), 0, s, a);
+    } else if (a.bias) {
+        hipLaunchKernelGGL((markov_segment_kernel<DT, false, true>), grid, dim3(kSelThreads), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((markov_segment_kernel<DT, false, false>), grid, dim3(kSelThreads), 0, s, a);
+    }
+    hipLaunchKernelGGL(markov_merge_kernel, dim3(static_cast<unsigned>(a.batch)), dim3(kSelThreads), 0, s, a);
+}
+
+extern "C" int nvs_markov_draw_workspace_size(int64_t batch, int64_t vocab, int num_candidates, size_t* bytes) {
+    nvs::clear_error();
+    NVS_CHECK(bytes != nullptr && batch >= 0 && vocab > 0 && num_candidates >= 1, NVS_ERR_INVALID,
+              "markov_draw_workspace_size: bad arguments");
+    int n_seg, seg_len;
+    markov_segments(vocab, &n_seg, &seg_len);
+    *bytes = markov_split(vocab, num_candidates)
+                 ? static_cast<size_t>(batch) * n_seg * num_candidates * sizeof(uint64_t) : 0;
+    return NVS_OK;
+}
+
+extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t logits_row_stride, const void* bias,
+                               int64_t bias_row_stride, int64_t batch, int64_t vocab, const float* temperatures,
+                               const int64_t* top_k, const float* top_p, int max_top_k, int has_top_p,
+                               int num_candidates, const float* noise, int64_t noise_row_stride, int32_t* cand_ids,
+                               float* cand_probs, int64_t cand_row_stride, int64_t* draws, int64_t draws_stride,
+                               void* workspace, size_t workspace_bytes, void* stream) {
     nvs::clear_error();
     int st = check_dtype(logits_dtype);
     if (st != NVS_OK) return st;
@@ -2101,7 +2501,49 @@ extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t log
     NVS_CHECK(noise_row_stride >= num_candidates && cand_row_stride >= num_candidates, NVS_ERR_INVALID,
               "markov_draw: a row stride is shorter than num_candidates");
     NVS_CHECK(draws_stride >= 1, NVS_ERR_INVALID, "markov_draw: draws_stride must be >= 1");
+    NVS_CHECK(bias == nullptr || bias_row_stride >= vocab, NVS_ERR_INVALID, "markov_draw: bias row stride < vocab");
+    NVS_CHECK(batch <= 65535, NVS_ERR_UNSUPPORTED, "markov_draw: batch %lld above 65535", (long long)batch);
     if (batch == 0) return NVS_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (markov_split(vocab, num_candidates)) {
+        MarkovSplitArgs m{};
+        markov_segments(vocab, &m.n_seg, &m.seg_len);
+        const size_t need = static_cast<size_t>(batch) * m.n_seg * num_candidates * sizeof(uint64_t);
+        NVS_CHECK(workspace != nullptr && workspace_bytes >= need, NVS_ERR_WORKSPACE,
+                  "markov_draw: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+        m.logits = logits;
+        m.row_stride = logits_row_stride;
+        m.bias = bias;
+        m.bias_stride = bias_row_stride;
+        m.batch = batch;
+        m.vocab = vocab;
+        m.temps = temperatures;
+        m.top_k = top_k;
+        m.top_p = top_p;
+        m.max_top_k = max_top_k;
+        m.has_top_p = has_top_p;
+        m.n_cand = num_candidates;
+        m.pairs = static_cast<uint64_t*>(workspace);
+        m.noise = noise;
+        m.noise_stride = noise_row_stride;
+        m.cand_ids = cand_ids;
+        m.cand_probs = cand_probs;
+        m.cand_stride = cand_row_stride;
+        m.draws = draws;
+        m.draws_stride = draws_stride;
+        const bool vec = vector_rows(logits, logits_row_stride, vocab, logits_dtype) &&
+                         (bias == nullptr || vector_rows(bias, bias_row_stride, vocab, logits_dtype));
+        switch (logits_dtype) {
+            case NVS_DTYPE_F32: launch_markov_split<NVS_DTYPE_F32>(m, vec, s); break;
+            case NVS_DTYPE_BF16: launch_markov_split<NVS_DTYPE_BF16>(m, vec, s); break;
+            default: launch_markov_split<NVS_DTYPE_F16>(m, vec, s); break;
+        }
+        return nvs::check_launch("markov draw kernels");
+    }
+    // more candidates than the split draw takes: one workgroup per sequence, on logits the caller has biased
+    NVS_CHECK(bias == nullptr, NVS_ERR_UNSUPPORTED,
+              "markov_draw: %d candidates take the unsplit draw, which needs the bias added beforehand",
+              num_candidates);
     SelArgs a{};
     a.logits = logits;
     a.row_stride = logits_row_stride;
@@ -2121,7 +2563,7 @@ extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t log
     a.cand_stride = cand_row_stride;
     a.draws = draws;
     a.draws_stride = draws_stride;
-    return launch_select<kModeMarkov>(logits_dtype, a, static_cast<hipStream_t>(stream));
+    return launch_select<kModeMarkov>(logits_dtype, a, s);
 }
 
 extern "C" int nvs_race_workspace_size(int64_t n_rows, int64_t vocab, size_t* bytes) {

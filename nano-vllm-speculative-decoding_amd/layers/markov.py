@@ -10,6 +10,7 @@ does not truncate) a row is drawn over the whole vocabulary with probs_from_logi
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import Callable
 
@@ -43,10 +44,13 @@ class CandidateRows:
 
 
 def markov_draw(row_logits: torch.Tensor, sampling: ss.SamplingTensors, candidates: int, noise: torch.Tensor,
-                ids: torch.Tensor, probs: torch.Tensor, draws: torch.Tensor) -> None:
-    """One candidate row for every sequence: row_logits [B, V] (already biased), noise [B, >= C] fp32 by candidate
-    rank. Writes ids [B, C] int32, probs [B, C] fp32 and draws [B] int64 (a column view of the drafts is fine)."""
-    _lib.require_device(row_logits, noise, ids, probs, draws, sampling.temperatures, sampling.top_k)
+                ids: torch.Tensor, probs: torch.Tensor, draws: torch.Tensor,
+                bias: torch.Tensor | None = None) -> None:
+    """One candidate row for every sequence: row_logits [B, V] (rows with unit element stride, any row stride),
+    bias [B, V] the row's Markov bias or None, noise [B, >= C] fp32 by candidate rank. Writes ids [B, C] int32,
+    probs [B, C] fp32 and draws [B] int64 (a column view of the drafts is fine). The kernel adds the bias with the
+    reference's rounding when it has the logits' dtype; otherwise torch adds it first (the reference's promotion)."""
+    _lib.require_device(row_logits, bias, noise, ids, probs, draws, sampling.temperatures, sampling.top_k)
     if sampling.temperatures is None:
         raise ValueError("greedy rows are drawn by argmax, not by markov_draw")
     if row_logits.dim() != 2 or row_logits.stride(-1) != 1:
@@ -59,15 +63,23 @@ def markov_draw(row_logits: torch.Tensor, sampling: ss.SamplingTensors, candidat
         raise ValueError("ids and probs must share their row stride")
     if draws.dtype != torch.int64 or draws.shape != (batch,):
         raise ValueError("draws must be [B] int64")
+    lib = _lib.load()
+    nbytes = _lib.size_out()
+    _lib.check(lib.nvs_markov_draw_workspace_size(batch, vocab, candidates, ctypes.byref(nbytes)),
+               "markov_draw_workspace_size")
+    if bias is not None and (bias.dtype != row_logits.dtype or bias.shape != row_logits.shape or nbytes.value == 0
+                             or bias.stride(-1) != 1):
+        row_logits, bias = row_logits + bias, None
     temps = ss._contig(sampling.temperatures, torch.float32)
     top_k = ss._contig(sampling.top_k, torch.int64)
     top_p = ss._contig(sampling.top_p, torch.float32)
-    lib = _lib.load()
+    ws = _lib.workspace(nbytes.value, row_logits.device)
     _lib.check(lib.nvs_markov_draw(row_logits.data_ptr(), _lib.dtype_code(row_logits.dtype), row_logits.stride(0),
-                                   batch, vocab, temps.data_ptr(), top_k.data_ptr(), _lib.ptr(top_p),
-                                   sampling.max_top_k, int(sampling.has_top_p), candidates, noise.data_ptr(),
-                                   noise.stride(0), ids.data_ptr(), probs.data_ptr(), ids.stride(0), draws.data_ptr(),
-                                   draws.stride(0), _lib.stream_of(row_logits)),
+                                   _lib.ptr(bias), 0 if bias is None else bias.stride(0), batch, vocab,
+                                   temps.data_ptr(), top_k.data_ptr(), _lib.ptr(top_p), sampling.max_top_k,
+                                   int(sampling.has_top_p), candidates, noise.data_ptr(), noise.stride(0),
+                                   ids.data_ptr(), probs.data_ptr(), ids.stride(0), draws.data_ptr(), draws.stride(0),
+                                   _lib.ptr(ws), nbytes.value, _lib.stream_of(row_logits)),
                "markov_draw")
 
 
@@ -83,15 +95,17 @@ def markov_rows(logits: torch.Tensor, prev: torch.Tensor, sampling: ss.SamplingT
                              torch.empty(batch, k, candidates, dtype=torch.float32, device=logits.device))
     q = None if greedy or candidates else torch.empty(batch, k, vocab, dtype=torch.float32, device=logits.device)
     for row in range(k):
-        row_logits = logits[:, row] + markov_bias(prev)
-        if greedy:
-            drafts[:, row] = row_logits.argmax(dim=-1)
-        elif candidates:
-            markov_draw(row_logits, sampling, candidates, noise[:, row], rows.ids[:, row], rows.probs[:, row],
-                        drafts[:, row])
+        if candidates and not greedy:
+            # the kernel reads the row of the block's logits and the bias, and adds them itself
+            markov_draw(logits[:, row], sampling, candidates, noise[:, row], rows.ids[:, row], rows.probs[:, row],
+                        drafts[:, row], bias=markov_bias(prev))
         else:
-            q[:, row] = ss.probs_from_logits(row_logits, sampling)
-            drafts[:, row] = ss.race(q[:, row], noise[:, row])
+            row_logits = logits[:, row] + markov_bias(prev)
+            if greedy:
+                drafts[:, row] = row_logits.argmax(dim=-1)
+            else:
+                q[:, row] = ss.probs_from_logits(row_logits, sampling)
+                drafts[:, row] = ss.race(q[:, row], noise[:, row])
         prev = drafts[:, row]
     if greedy:
         return None
