@@ -361,9 +361,13 @@ def markov_bench(args, dev):
     ms_d = time_gpu(graphed(draw_only), steps, warm)
     ms_b = time_gpu(graphed(bias_only), steps, warm)
     same = bool(torch.equal(drafts, drafts_t))
+    replayed = drafts.clone()
+    ours()                     # eager, on the same inputs: the graph's replays must have drawn the same tokens
+    same = same and bool(torch.equal(drafts, replayed))
     alg = 2 * B * V * 2        # one read of a row's bf16 logits and of its bf16 bias per draw
     log(f"[bench] DSpark propose sampling (7 Markov rows, B 64, V 151936 bf16, 84 candidates, HIP graphs): "
-        f"{ms * 1e3:.1f} us vs {ms_t * 1e3:.1f} us as torch ops with dense q (same drafts: {same}); one draw "
+        f"{ms * 1e3:.1f} us vs {ms_t * 1e3:.1f} us as torch ops with dense q (same drafts, graph and eager: {same}); "
+        f"one draw "
         f"{ms_d * 1e3:.2f} us ({alg / (ms_d * 1e-3) / 1e9:.0f} GB/s with its bias), Markov head GEMM {ms_b * 1e3:.2f} us")
     return {"workload": "markov_rows_b64_k7_v151936_bf16_topk20_rank64", "us": round(ms * 1e3, 2),
             "torch_ops_dense_q_us": round(ms_t * 1e3, 2), "same_drafts": same, "draw_us": round(ms_d * 1e3, 2),

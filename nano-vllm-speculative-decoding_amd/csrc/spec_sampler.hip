@@ -1183,6 +1183,7 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_segment_kernel(MarkovSp
     __shared__ uint32_t hist[256];
     __shared__ int n_gt;
     __shared__ uint32_t pick_bin, pick_rem;
+    __shared__ uint64_t seg_pairs[kSplitMaxCand];   // the segment's want pairs, before they are sorted
     __shared__ uint32_t wbound[kSelWaves], whi[kSelWaves];
     constexpr int W = piece_elems<DT>();
     const int seg = blockIdx.x;
@@ -1356,8 +1357,8 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_segment_kernel(MarkovSp
         const uint32_t k = kr[q];
         if (q < qlim && want > 0 && k > t_key) {
             const int i = (static_cast<int>(threadIdx.x) + (q / W) * kSelThreads) * W + q % W;
-            out[atomicAdd(&n_gt, 1)] = (static_cast<uint64_t>(k) << 32) |
-                                       (0xffffffffu - static_cast<uint32_t>(e_lo + i));
+            seg_pairs[atomicAdd(&n_gt, 1)] = (static_cast<uint64_t>(k) << 32) |
+                                             (0xffffffffu - static_cast<uint32_t>(e_lo + i));
         }
     }
     __syncthreads();
@@ -1380,15 +1381,23 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_segment_kernel(MarkovSp
             if (q < qlim && want > 0 && kr[q] == t_key) {
                 if (r < need) {
                     const int i = (static_cast<int>(threadIdx.x) + j * kSelThreads) * W + c;
-                    out[gt + r] = (static_cast<uint64_t>(t_key) << 32) |
-                                  (0xffffffffu - static_cast<uint32_t>(e_lo + i));
+                    seg_pairs[gt + r] = (static_cast<uint64_t>(t_key) << 32) |
+                                        (0xffffffffu - static_cast<uint32_t>(e_lo + i));
                 }
                 ++r;
             }
         }
         base += total_j;
     }
-    // empty slots (a segment with fewer values than candidates) hold 0, below every pair
+    // the segment's list, sorted: each pair goes to its rank among the want pairs (all distinct); empty slots (a
+    // segment with fewer values than candidates) hold 0, below every pair
+    __syncthreads();
+    for (int p = threadIdx.x; p < want; p += kSelThreads) {
+        const uint64_t v = seg_pairs[p];
+        int above = 0;
+        for (int q = 0; q < want; ++q) above += (seg_pairs[q] > v) ? 1 : 0;
+        out[above] = v;
+    }
     for (int p = want + threadIdx.x; p < a.n_cand; p += kSelThreads) out[p] = 0ull;
 }
 
@@ -1398,13 +1407,12 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_merge_kernel(MarkovSpli
     uint64_t* pairs = pair_buf(sh);
     const int total = a.n_seg * a.n_cand;
     const int C = a.n_cand;
-    // The union of the segments' pairs goes to the upper half of the pair space. Every pair is distinct (one index
-    // each), except the zeros of empty slots. The want-th largest pair is found by a radix select on the keys,
-    // then on the low words of the pairs tied at that key. The pairs at or above it, exactly `want`, go to
-    // [512, 1024), and each is placed at its rank among them in [0, n_cand).
+    // The segments' lists, each sorted (value descending, index ascending, zeros of empty slots last), go to the
+    // upper half of the pair space. A pair's rank in the union is its place in its own list plus, for every other
+    // list, the number of its pairs above it (a binary search): every pair is distinct (one index each). The first
+    // n_cand ranks go straight to their place in the lower half.
     const uint64_t* src = a.pairs + b * total;
     uint64_t* all = pairs + kPairCap / 2;
-    uint64_t* sel = pairs + kSplitMaxCand;
     int nz = 0;
     for (int i = threadIdx.x; i < total; i += kSelThreads) {
         const uint64_t v = src[i];
@@ -1414,35 +1422,26 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_merge_kernel(MarkovSpli
     for (int i = threadIdx.x; i < C; i += kSelThreads) pairs[i] = 0ull;
     nz = static_cast<int>(block_sum(static_cast<float>(nz), sh));   // its barriers publish `all`
     const int want = min(C, nz);
-    if (want > 0) {
-        uint32_t ng, ne;
-        auto each_key = [&](auto&& fn) {
-            for (int i = threadIdx.x; i < total; i += kSelThreads)
-                if (all[i] != 0ull) fn(static_cast<uint32_t>(all[i] >> 32));
-        };
-        const uint32_t t_key = radix_select(each_key, static_cast<uint32_t>(want), sh, &ng, &ne);
-        auto each_low = [&](auto&& fn) {
-            for (int i = threadIdx.x; i < total; i += kSelThreads) {
-                const uint64_t v = all[i];
-                if (v != 0ull && static_cast<uint32_t>(v >> 32) == t_key) fn(static_cast<uint32_t>(v));
+    for (int i = threadIdx.x; i < total; i += kSelThreads) {
+        const uint64_t v = all[i];
+        if (v == 0ull) continue;
+        const int own = i / C;
+        int rank = i - own * C;
+        for (int s1 = 0; s1 < a.n_seg && rank < C; ++s1) {
+            if (s1 == own) continue;
+            const uint64_t* list = all + s1 * C;
+            int lo = 0, hi = C;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (list[mid] > v) {
+                    lo = mid + 1;
+                } else {
+                    hi = mid;
+                }
             }
-        };
-        uint32_t ng2, ne2;
-        const uint32_t t_low = radix_select(each_low, static_cast<uint32_t>(want) - ng, sh, &ng2, &ne2);
-        const uint64_t t_pair = (static_cast<uint64_t>(t_key) << 32) | t_low;
-        if (threadIdx.x == 0) sh.count = 0;
-        __syncthreads();
-        for (int i = threadIdx.x; i < total; i += kSelThreads) {
-            const uint64_t v = all[i];
-            if (v != 0ull && v >= t_pair) sel[atomicAdd(&sh.count, 1)] = v;
+            rank += lo;
         }
-        __syncthreads();
-        for (int i = threadIdx.x; i < want; i += kSelThreads) {
-            const uint64_t v = sel[i];
-            int above = 0;
-            for (int j = 0; j < want; ++j) above += (sel[j] > v) ? 1 : 0;
-            pairs[above] = v;
-        }
+        if (rank < C) pairs[rank] = v;
     }
     __syncthreads();
     const int real = want;
