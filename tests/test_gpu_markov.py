@@ -184,3 +184,36 @@ def test_accept_on_candidate_rows_equals_the_dense_q(device, top_k, top_p, varle
         want = ss.accept_random(p.view(batch, k + 1, vocab), dense.cpu(), drafts.cpu(), uniforms.cpu(), noise.cpu())
     assert torch.equal(n_s.cpu(), want[0]) and torch.equal(t_s.cpu(), want[1]), "the oracle disagrees"
     print(f"mean accepted {float(n_s.float().mean()):.2f}")
+
+
+def test_markov_rows_replay_in_a_graph(device):
+    """The rows as the reference's sampling graphs run them: captured once, replayed with the noise refreshed
+    outside the graph, eager work between the replays, every replay equal to the eager rows on the same noise."""
+    log_case("markov rows: HIP graph replay")
+    batch, k, vocab = 8, 7, 151936
+    g = torch.Generator(device=device).manual_seed(31)
+    logits = (torch.randn(batch, k, vocab, device=device, generator=g) * 3).to(torch.bfloat16)
+    w1 = torch.randn(vocab, 16, device=device, generator=g, dtype=torch.bfloat16) * 0.1
+    w2 = torch.randn(vocab, 16, device=device, generator=g, dtype=torch.bfloat16) * 0.1
+    bias = lambda prev: torch.nn.functional.linear(torch.nn.functional.embedding(prev, w1), w2)
+    st = sampling(device, [1.0, 0.7] * (batch // 2), [20, 5] * (batch // 2), [1.0, 0.9] * (batch // 2))
+    C = nm.num_candidates(st.max_top_k, st.all_top_k, vocab)
+    anchors = torch.arange(batch, device=device)
+    noise = torch.empty(batch, k, C, device=device)
+    drafts = torch.empty(batch, k, dtype=torch.int64, device=device)
+    ns.exponential_noise_(noise, g)
+    rows = nm.markov_rows(logits, anchors, st, bias, noise, drafts, C)   # warm-up, outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rows = nm.markov_rows(logits, anchors, st, bias, noise, drafts, C)
+    for replay in range(3):
+        ns.exponential_noise_(noise, g)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (drafts.clone(), rows.ids.clone(), rows.probs.clone())
+        want_drafts = torch.empty_like(drafts)
+        want = nm.markov_rows(logits, anchors, st, bias, noise, want_drafts, C)
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], want_drafts), f"replay {replay}: drafts differ from the eager rows"
+        assert torch.equal(got[1], want.ids) and torch.equal(got[2], want.probs), f"replay {replay}: candidate rows"
