@@ -493,7 +493,7 @@ def main():
                     help="also time a plain 1 GiB device copy (the counter scale for rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one MI355X: the verify hot path runs on one GPU's share and this build has no "
+        print("bench.py measures one MI355X: the verify hot path runs on one GPU's share and this library has no "
               "multi-GPU path; run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
 

@@ -1,5 +1,6 @@
 """Oracle of the decoder layer's elementwise ops: RMSNorm (with the residual add) and SiLU-and-mul, in eager torch
-on the CPU, op by op as the reference writes them. TEST INFRASTRUCTURE: only tests/ use it, as the checker.
+on the CPU, op by op as the reference writes them. TEST INFRASTRUCTURE: only tests/ use it, to compare the kernels
+against.
 
 Reference: RMSNorm.rms_forward / add_rms_forward (nanovllm/layers/layernorm.py:15-40), SiluAndMul.forward
 (nanovllm/layers/activation.py:8-11). The reference runs both under torch.compile, which keeps the fp32

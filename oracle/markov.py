@@ -1,4 +1,4 @@
-"""Oracle of DSpark's Markov rows: TEST INFRASTRUCTURE (tests only, as the checker).
+"""Oracle of DSpark's Markov rows: TEST INFRASTRUCTURE (only tests/ use it, to compare the kernels against).
 
 Restates DFlashDrafter._sample_markov / _markov_rows (nanovllm/engine/speculative.py:145-184) and num_candidates
 (:46-50) on the CPU with the oracle's sampler functions. The Markov head is a function prev -> [B, V] bias, as the
