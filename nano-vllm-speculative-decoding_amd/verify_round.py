@@ -86,6 +86,7 @@ class VerifyBatch:
     block_tables: list[list[int]]
     num_blocks: int               # blocks in use; the pad block (zeros) is block num_blocks
     block_size: int = 256
+    last_tokens: list[int] | None = None   # each row's last token (the first verified input), when known
 
     @property
     def pad_block(self) -> int:
@@ -119,12 +120,16 @@ def random_verify_batch(batch: int, q_range: tuple[int, int] = (1, 8), k_range: 
 
 @dataclass
 class VerifyMetadata:
-    """One verify forward over its row slots (batch_metadata.py:127-139 without the draft placement)."""
+    """One verify forward over its row slots (batch_metadata.py:127-139). input_ids holds each row's last token
+    (0 when unknown) and 0 at the draft positions, which draft_index / draft_source fill from the drafts [B, k]."""
+    input_ids: list[int] = field(default_factory=list)
     positions: list[int] = field(default_factory=list)
     slot_mapping: list[int] = field(default_factory=list)
     cu_seqlens_q: list[int] = field(default_factory=lambda: [0])
     cu_seqlens_k: list[int] = field(default_factory=lambda: [0])
     block_tables: list[list[int]] = field(default_factory=list)
+    draft_index: list[int] = field(default_factory=list)
+    draft_source: list[int] = field(default_factory=list)
 
 
 def verify_varlen_metadata(batch: VerifyBatch | None, num_rows: int, num_tokens: int, width: int,
@@ -141,10 +146,16 @@ def verify_varlen_metadata(batch: VerifyBatch | None, num_rows: int, num_tokens:
     block_size = 256 if batch is None else batch.block_size
     if len(rows) > num_rows:
         raise ValueError(f"{len(rows)} rows do not fit {num_rows} row slots")
-    for q_len, k_len, table in rows:
+    num_drafts = query_len - 1
+    for r, (q_len, k_len, table) in enumerate(rows):
         start = k_len - q_len
         if not 1 <= q_len <= query_len or len(table) > width or len(table) * block_size < k_len:
             raise ValueError("a row's verify length, context or block table does not fit the graph")
+        first = len(md.positions)
+        last = batch.last_tokens[r] if batch.last_tokens is not None else 0
+        md.input_ids.extend([last] + [0] * (q_len - 1))
+        md.draft_index.extend(range(first + 1, first + q_len))
+        md.draft_source.extend(range(r * num_drafts, r * num_drafts + q_len - 1))
         md.positions.extend(range(start, k_len))
         md.slot_mapping.extend(table[p // block_size] * block_size + p % block_size for p in range(start, k_len))
         md.cu_seqlens_q.append(md.cu_seqlens_q[-1] + q_len)
@@ -156,6 +167,7 @@ def verify_varlen_metadata(batch: VerifyBatch | None, num_rows: int, num_tokens:
     for _ in range(num_rows - len(rows)):
         n = min(left, query_len)
         left -= n
+        md.input_ids.extend([0] * n)
         md.positions.extend(range(n))
         md.slot_mapping.extend([PAD_SLOT] * n)
         md.cu_seqlens_q.append(md.cu_seqlens_q[-1] + n)

@@ -62,3 +62,47 @@ def test_random_batch_and_weight_bytes():
     assert blocks == list(range(batch.num_blocks))                  # a permutation: every block used once
     assert all(len(t) * 256 >= k for t, k in zip(batch.block_tables, batch.k_lens))
     assert vr.QWEN3_8B.streamed_weight_bytes() == 15_136_194_560   # 36 layers + LM head in bf16
+
+
+def reference_row(length: int, table: list[int], verified: int):
+    """A sequence of `length` tokens verifying `verified` of them from position length - 1, as the reference's
+    tests build it (make_sequence): in this layout q_len = verified and k_len = length - 1 + verified."""
+    return verified, length - 1 + verified, table
+
+
+def test_reference_verify_metadata_known_answers():
+    # tests/test_batch_metadata.py:68-77: len 5 on blocks [7, 8, 9], k = 2, two slots of 3 tokens, block size 4
+    q, k, t = reference_row(5, [7, 8, 9], 3)
+    md = vr.verify_varlen_metadata(vr.VerifyBatch([q], [k], [t], num_blocks=99, block_size=4, last_tokens=[4]),
+                                   num_rows=2, num_tokens=6, width=3, query_len=3)
+    assert md.input_ids == [4, 0, 0, 0, 0, 0]
+    assert md.positions == [4, 5, 6, 0, 1, 2]
+    assert md.slot_mapping == [32, 33, 34, -1, -1, -1]
+    assert md.cu_seqlens_q == [0, 3, 6] and md.cu_seqlens_k == [0, 7, 10]
+    assert md.block_tables == [[7, 8, 9], [99, 99, 99]]
+    # :80-84: a short block table is padded with the pad block
+    q, k, t = reference_row(2, [4], 2)
+    md = vr.verify_varlen_metadata(vr.VerifyBatch([q], [k], [t], num_blocks=99, block_size=4),
+                                   num_rows=1, num_tokens=2, width=2, query_len=2)
+    assert md.block_tables == [[4, 99]]
+
+
+def test_reference_varlen_metadata_known_answers():
+    # tests/test_batch_metadata.py:124-134: rows of len 100 (block 7) and 37 (block 3) verify 5 and 3 tokens, k = 7
+    rows = [reference_row(100, [7], 5), reference_row(37, [3], 3)]
+    batch = vr.VerifyBatch([r[0] for r in rows], [r[1] for r in rows], [r[2] for r in rows], num_blocks=99,
+                           block_size=256, last_tokens=[99, 36])
+    md = vr.verify_varlen_metadata(batch, num_rows=2, num_tokens=8, width=1, query_len=8)
+    assert md.input_ids == [99, 0, 0, 0, 0, 36, 0, 0]
+    assert md.positions == [99, 100, 101, 102, 103, 36, 37, 38]
+    assert md.slot_mapping == [1891, 1892, 1893, 1894, 1895, 804, 805, 806]
+    assert md.cu_seqlens_q == [0, 5, 8] and md.cu_seqlens_k == [0, 104, 143]
+    assert md.draft_index == [1, 2, 3, 4, 6, 7] and md.draft_source == [0, 1, 2, 3, 7, 8]
+    # :137-146: one row of 3 in 9 tokens and 4 slots, k = 3: padding rows of 4 and 2, then an empty slot
+    q, k, t = reference_row(5, [7, 8], 3)
+    md = vr.verify_varlen_metadata(vr.VerifyBatch([q], [k], [t], num_blocks=99, block_size=4),
+                                   num_rows=4, num_tokens=9, width=2, query_len=4)
+    assert md.positions == [4, 5, 6, 0, 1, 2, 3, 0, 1]
+    assert md.slot_mapping == [32, 33, 34] + [vr.PAD_SLOT] * 6
+    assert md.cu_seqlens_q == [0, 3, 7, 9, 9] and md.cu_seqlens_k == [0, 7, 11, 13, 13]
+    assert md.block_tables == [[7, 8], [99, 99], [99, 99], [99, 99]]
