@@ -274,6 +274,17 @@ class Qwen3VerifyTarget:
         return F.linear(hidden, self.lm_head)
 
 
+def place_drafts(input_ids: torch.Tensor, drafts: torch.Tensor, md: VerifyMetadata) -> None:
+    """The verified drafts into the flat input ids where the metadata puts them (speculative.py:514-517):
+    input_ids[draft_index] = drafts.flatten()[draft_source]."""
+    if not md.draft_index:
+        return
+    dev = input_ids.device
+    index = torch.tensor(md.draft_index, dtype=torch.int64).to(dev, non_blocking=True)
+    source = torch.tensor(md.draft_source, dtype=torch.int64).to(dev, non_blocking=True)
+    input_ids[index] = drafts.reshape(-1).to(input_ids.dtype)[source]
+
+
 class VerifyGraphs:
     """One HIP graph of the target's forward per (row slots, tokens) shape of verify_token_counts, over static
     device buffers, all in one memory pool (speculative.py:530-572). A round builds its metadata on the host,
@@ -308,6 +319,24 @@ class VerifyGraphs:
     def _context(self, num_rows: int, num_tokens: int) -> VerifyContext:
         return VerifyContext(self.cu_seqlens_q[:num_rows + 1], self.cu_seqlens_k[:num_rows + 1], self.query_len,
                              self.max_model_len, self.slot_mapping[:num_tokens], self.block_tables[:num_rows])
+
+    @torch.inference_mode()
+    def run_drafts(self, batch: VerifyBatch, drafts: torch.Tensor) -> torch.Tensor:
+        """run() with the input ids built from the metadata (speculative.py:502-512): each row's last token
+        (batch.last_tokens) and its verified drafts from drafts [B, k], placed by draft_index / draft_source."""
+        if batch.last_tokens is None:
+            raise ValueError("run_drafts needs each row's last token")
+        num_rows, num_tokens = self.shape_for(batch.num_tokens)
+        if num_tokens not in self.graphs:
+            self.capture([num_tokens])
+        md = verify_varlen_metadata(batch, num_rows, num_tokens, self.width, self.query_len)
+        self._load(md, num_rows, num_tokens)
+        self.input_ids[:num_tokens].copy_(torch.tensor(md.input_ids, dtype=torch.int64,
+                                                       pin_memory=self.target.device.type == "cuda"),
+                                          non_blocking=True)
+        place_drafts(self.input_ids, drafts, md)
+        self.graphs[num_tokens].replay()
+        return self.outputs[:batch.num_tokens]
 
     def _load(self, md: VerifyMetadata, num_rows: int, num_tokens: int) -> None:
         """Host metadata into the buffers (speculative.py:519-529): pinned host tensors, asynchronous copies."""

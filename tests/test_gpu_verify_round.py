@@ -169,3 +169,26 @@ def test_graph_replay_matches_eager(device):
     got = graphs.run(other, ids).clone()
     assert torch.equal(got, graphs.run_eager(other, ids))
     assert len(graphs.graphs) == 1
+
+
+@pytest.mark.gpu
+def test_run_drafts_places_the_drafts_like_the_host_layout(device):
+    log_case("verify graph with drafts placed from the metadata, 2 small Qwen3 layers")
+    batch, target, _ = small_setup(device, seed=2)
+    k = 7
+    gen = torch.Generator().manual_seed(5)
+    batch.last_tokens = torch.randint(0, SMALL.vocab_size, (len(batch.q_lens),), generator=gen).tolist()
+    drafts = torch.randint(0, SMALL.vocab_size, (len(batch.q_lens), k), generator=gen)
+    md = vr.verify_varlen_metadata(batch, len(batch.q_lens), batch.num_tokens, 16, k + 1)
+    ids = torch.tensor(md.input_ids)
+    vr.place_drafts(ids, drafts, md)
+    start = 0
+    for r, q_len in enumerate(batch.q_lens):   # each row: its last token, then its first q_len - 1 drafts
+        assert ids[start:start + q_len].tolist() == [batch.last_tokens[r]] + drafts[r, :q_len - 1].tolist()
+        start += q_len
+    graphs = vr.VerifyGraphs(target, max_batch_size=8, query_len=k + 1, max_model_len=1024)
+    want = graphs.run(batch, ids.to(device)).clone()
+    for _ in range(2):
+        got = graphs.run_drafts(batch, drafts.to(device)).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)

@@ -2,6 +2,7 @@
 answers of the reference's tests/test_verify_schedule.py:54-55), the row-slot metadata (batch_metadata.py:149-181)
 on a hand-worked example, and the weight bytes of the Qwen3-8B shape."""
 import pytest
+import torch
 
 from nvs_amd import verify_round as vr
 
@@ -106,3 +107,40 @@ def test_reference_varlen_metadata_known_answers():
     assert md.slot_mapping == [32, 33, 34] + [vr.PAD_SLOT] * 6
     assert md.cu_seqlens_q == [0, 3, 7, 9, 9] and md.cu_seqlens_k == [0, 7, 11, 13, 13]
     assert md.block_tables == [[7, 8], [99, 99], [99, 99], [99, 99]]
+
+
+def test_reference_verify_round_layout_known_answers():
+    # tests/test_speculative_decoder.py:16-17,124-133: block size 4, k = 3; prompt [8, 9, 10] + 11 on blocks [3, 4]
+    # verifies 11 and the drafts 12, 13, 14
+    q, k, t = reference_row(4, [3, 4], 4)
+    batch = vr.VerifyBatch([q], [k], [t], num_blocks=99, block_size=4, last_tokens=[11])
+    md = vr.verify_varlen_metadata(batch, num_rows=1, num_tokens=4, width=2, query_len=4)
+    ids = torch.tensor(md.input_ids)
+    vr.place_drafts(ids, torch.tensor([[12, 13, 14]]), md)
+    assert ids.tolist() == [11, 12, 13, 14]
+    assert md.positions == [3, 4, 5, 6] and md.slot_mapping == [15, 16, 17, 18]
+    assert md.cu_seqlens_q == [0, 4] and md.cu_seqlens_k == [0, 7] and md.block_tables == [[3, 4]]
+    # :160-173: the same row verifying 2, and [1, 2, 3] + 4 on blocks [8, 9] verifying 4; drafts [5, 0, 1]
+    rows = [reference_row(4, [3, 4], 2), reference_row(4, [8, 9], 4)]
+    batch = vr.VerifyBatch([r[0] for r in rows], [r[1] for r in rows], [r[2] for r in rows], num_blocks=99,
+                           block_size=4, last_tokens=[11, 4])
+    md = vr.verify_varlen_metadata(batch, num_rows=2, num_tokens=6, width=2, query_len=4)
+    ids = torch.tensor(md.input_ids)
+    vr.place_drafts(ids, torch.tensor([[12, 13, 14], [5, 0, 1]]), md)
+    assert ids.tolist() == [11, 12, 4, 5, 0, 1] and md.positions == [3, 4, 3, 4, 5, 6]
+    assert md.slot_mapping == [15, 16, 35, 36, 37, 38]
+    assert md.cu_seqlens_q == [0, 2, 6] and md.cu_seqlens_k == [0, 5, 12]
+
+
+def test_reference_graph_inputs_known_answer():
+    # tests/test_speculative_decoder.py:176-189: a graph of 8 tokens and 4 slots, rows verifying 2 and 3
+    rows = [reference_row(4, [3, 4], 2), reference_row(4, [8, 9], 3)]
+    batch = vr.VerifyBatch([r[0] for r in rows], [r[1] for r in rows], [r[2] for r in rows], num_blocks=99,
+                           block_size=4, last_tokens=[11, 4])
+    md = vr.verify_varlen_metadata(batch, num_rows=4, num_tokens=8, width=2, query_len=4)
+    ids = torch.zeros(32, dtype=torch.int64)
+    ids[:8] = torch.tensor(md.input_ids)
+    vr.place_drafts(ids, torch.tensor([[12, 13, 14], [5, 0, 1]]), md)
+    assert ids[:8].tolist() == [11, 12, 4, 5, 0, 0, 0, 0]
+    assert md.cu_seqlens_q[:5] == [0, 2, 5, 8, 8]
+    assert md.block_tables == [[3, 4], [8, 9], [99, 99], [99, 99]]
