@@ -30,8 +30,9 @@ METRIC = "verify-attn µs/layer & HBM GB/s (% of 8 TB/s) at B=64, 8 q, 3k ctx"
 # by what the counter reads for the 1 GiB copy probe (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); the runs and their
 # numbers are in profiles/hbm_traffic_pmc_verify_attention_and_spec_accept.md. Re-measure after a kernel change.
 MEASURED_TRAFFIC = {
-    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200": 789_784_400,
-    "spec_accept_b64_k7_v151936_fp32_topk64": 320_062_639,
+    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200": 789_768_455,              # head-major caches
+    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_token_major": 789_781_254,
+    "spec_accept_b64_k7_v151936_fp32_topk64": 320_078_949,
 }
 
 
@@ -75,21 +76,34 @@ def attention_bench(args, dev):
 
     log("[bench] building the batch-64 verify-attention workload")
     case = wl.config_c3()
-    g = case.to(dev)
     max_k = 4096
-    out = torch.empty_like(g.q)
-    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
-
-    def step():
-        nattn._paged_attention(g.q, g.k_cache, g.v_cache, g.block_tables, g.cu_seqlens_q, g.cu_seqlens_k, None, 0,
-                               len(case.q_lens), g.max_seqlen_q, max_k, g.scale, True, out=out, workspace=ws)
-
-    ms = time_gpu(step, args.steps, args.warmup)
     kv, qo = case.kv_bytes(), case.qo_bytes()
-    gbs = (kv + qo) / (ms * 1e-3) / 1e9
     flops = case.flops()
-    log(f"[bench] attention: {ms * 1e3:.1f} us/layer, {gbs:.0f} GB/s = {100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
-    return case, ms, kv + qo, gbs, flops
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    # The reference's token-major layout (model_runner.py:160), then the library's head-major layout (each
+    # (block, kv head) one contiguous run): the same values through the same kernel.
+    timed = {}
+    for layout in ("token_major", "head_major"):
+        g = (case.head_major() if layout == "head_major" else case).to(dev)
+        out = torch.empty_like(g.q)
+
+        def step():
+            nattn._paged_attention(g.q, g.k_cache, g.v_cache, g.block_tables, g.cu_seqlens_q, g.cu_seqlens_k, None,
+                                   0, len(case.q_lens), g.max_seqlen_q, max_k, g.scale, True, out=out, workspace=ws)
+
+        ms = time_gpu(step, args.steps, args.warmup)
+        gbs = (kv + qo) / (ms * 1e-3) / 1e9
+        log(f"[bench] attention ({layout} cache): {ms * 1e3:.1f} us/layer, {gbs:.0f} GB/s = "
+            f"{100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
+        timed[layout] = (ms, gbs)
+        del g, out
+    ms, gbs = timed["head_major"]
+    tm_ms, tm_gbs = timed["token_major"]
+    token_major = {"workload": "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200",
+                   "kv_layout": "token_major [blocks, 256, 8, 128] (the reference's)", "us": round(tm_ms * 1e3, 2),
+                   "GBs": round(tm_gbs, 1), "frac": round(tm_gbs / HBM_PEAK_GBS, 4),
+                   "traffic": MEASURED_TRAFFIC["verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_token_major"]}
+    return case, ms, kv + qo, gbs, flops, token_major
 
 
 def launch_bound_bench(args, dev):
@@ -99,7 +113,7 @@ def launch_bound_bench(args, dev):
     import nvs_amd.workloads as wl
     from nvs_amd.layers import attention as nattn
     case = wl.config_c2()
-    g = case.to(dev)
+    g = case.head_major().to(dev)
     out = torch.empty_like(g.q)
     ws = torch.empty(16 << 20, dtype=torch.uint8, device=dev)
 
@@ -109,7 +123,8 @@ def launch_bound_bench(args, dev):
 
     ms = time_gpu(step, args.steps, args.warmup)
     b = case.kv_bytes() + case.qo_bytes()
-    return {"workload": "verify_attention_qwen3_8b_b8_ctx900_1200", "us": round(ms * 1e3, 2),
+    return {"workload": "verify_attention_qwen3_8b_b8_ctx900_1200", "kv_layout": "head_major",
+            "us": round(ms * 1e3, 2),
             "GBs": round(b / (ms * 1e-3) / 1e9, 1), "bytes": b}
 
 
@@ -206,7 +221,7 @@ def draft_block_bench(args, dev):
     lq = 7
     _, k_lens = wl.random_lengths(64, (1, 8), (2800 + lq, 3200 + lq), seed=1)
     case = wl.verify_attention_case([lq] * 64, k_lens, 32, 8, 128, pad_tokens_to=1)
-    g = case.to(dev)
+    g = case.head_major().to(dev)
     ctx = torch.tensor(k_lens, dtype=torch.int32, device=dev)
     out = torch.empty_like(g.q)
     ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
@@ -220,7 +235,8 @@ def draft_block_bench(args, dev):
     gbs = b / (ms * 1e-3) / 1e9
     log(f"[bench] draft-block attention (Lq 7, non-causal): {ms * 1e3:.1f} us, {gbs:.0f} GB/s = "
         f"{100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
-    return {"workload": "draft_block_attention_qwen3_8b_b64_lq7_noncausal_ctx2807_3207", "us": round(ms * 1e3, 2),
+    return {"workload": "draft_block_attention_qwen3_8b_b64_lq7_noncausal_ctx2807_3207", "kv_layout": "head_major",
+            "us": round(ms * 1e3, 2),
             "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": b}
 
 
@@ -507,8 +523,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
 
-    case, ms, nbytes, gbs, flops = attention_bench(args, dev)
-    extra = {"c2": launch_bound_bench(args, dev), "draft_block": draft_block_bench(args, dev),
+    case, ms, nbytes, gbs, flops, token_major = attention_bench(args, dev)
+    extra = {"attention_token_major": token_major, "c2": launch_bound_bench(args, dev),
+             "draft_block": draft_block_bench(args, dev),
              "qk_norm_rope_store": qk_rope_bench(args, dev)}
     if args.sampler == "on":
         extra["sampler"] = sampler_bench(args, dev)
@@ -534,7 +551,8 @@ def main():
         "data": "synthetic",
         "config": {"workload": "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200",
                    "rows": len(case.q_lens), "tokens": int(sum(case.q_lens)), "heads": "32q/8kv",
-                   "head_dim": 128, "block_size": 256, "max_seqlen_k": 4096},
+                   "head_dim": 128, "block_size": 256, "max_seqlen_k": 4096,
+                   "kv_layout": "head_major: [blocks, 256, 8, 128] view of [blocks, 8, 256, 128] memory"},
         "us_per_layer": round(ms * 1e3, 2),
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NVS_ABI_VERSION 5
+#define NVS_ABI_VERSION 6
 
 typedef enum {
     NVS_OK = 0,
@@ -55,16 +55,22 @@ const char* nvs_last_error(void);
 /* ------------------------------------------------------------------------------------------------ KV store
  * Replaces store_kvcache / store_kvcache_kernel (nanovllm/layers/attention.py:10-40; semantics restated in
  * tests/fake_paged_attention.py:14-17).
+ * Cache geometry (shared by every entry point that writes the cache): both caches are
+ * [cache_blocks, block_size, n_kv_heads, head_dim] with element strides cache_block_stride, cache_token_stride,
+ * cache_head_stride and a contiguous head_dim; slot s is token s % block_size of block s / block_size. The
+ * reference's token-major layout (model_runner.py:160) has strides (block_size*n_kv_heads*head_dim,
+ * n_kv_heads*head_dim, head_dim); a head-major cache [cache_blocks, n_kv_heads, block_size, head_dim], in which the
+ * attention streams each (block, head) as one contiguous run, has (n_kv_heads*block_size*head_dim, head_dim,
+ * block_size*head_dim).
  * For i < n_tokens with s = slot_mapping[i] >= 0 (the reference skips exactly s == -1; negative slots and slots
- * >= cache_slots are skipped here too instead of writing out of bounds):
- *   k_cache[s*row + e] = key[i*key_row_stride + e], v_cache[s*row + e] = value[i*value_row_stride + e],
- * for e < row = n_kv_heads*head_dim. Each token row of key/value must be contiguous (the reference asserts
- * stride(-1) == 1 and stride(1) == head_dim); value may be a strided view (a slice of the fused qkv output).
- * The caches are [cache_slots/block_size, block_size, n_kv_heads, head_dim] with contiguous slots. A pure copy:
- * bit-exact for every dtype. */
+ * >= cache_blocks*block_size are skipped here too instead of writing out of bounds), for every head h and e < head_dim:
+ *   k_cache[block(s), token(s), h, e] = key[i*key_row_stride + h*head_dim + e], and v_cache likewise from value.
+ * Each token row of key/value must be contiguous (the reference asserts stride(-1) == 1 and stride(1) == head_dim);
+ * value may be a strided view (a slice of the fused qkv output). A pure copy: bit-exact for every dtype. */
 int nvs_store_kvcache(const void* key, int64_t key_row_stride,
                       const void* value, int64_t value_row_stride,
-                      void* k_cache, void* v_cache, int64_t cache_slots,
+                      void* k_cache, void* v_cache, int64_t cache_blocks, int64_t block_size,
+                      int64_t cache_block_stride, int64_t cache_token_stride, int64_t cache_head_stride,
                       const int32_t* slot_mapping, int64_t n_tokens,
                       int n_kv_heads, int head_dim, int dtype, void* stream);
 
@@ -82,15 +88,18 @@ int nvs_store_kvcache(const void* key, int64_t key_row_stride,
  *   p = positions[t] (clamped into [0, cache_positions)), o = dtype(concat(y1*c - y2*s, y2*c + y1*s)), every
  *   product and sum rounded separately as in the eager ops.
  * q_out[t, h] = o for query heads (q_out may alias q); for key heads o goes to k_out (when non-NULL) and, like v, to
- * cache slot slot_mapping[t] (skipped when negative or >= cache_slots, as store_kvcache skips -1).
+ * cache slot slot_mapping[t] (skipped when negative or >= cache_blocks*block_size, as store_kvcache skips -1).
  * q, k, v, q_out, k_out: [n_tokens, heads, 128] with the given token strides and head stride 128 (views of the fused
  * qkv output are fine); weights [128] in the same dtype; cos_sin_cache [cache_positions, 128] fp32 (the
- * reference's cos_sin_cache buffer); caches [cache_slots, n_kv_heads, 128]. dtype bf16 or fp16. */
+ * reference's cos_sin_cache buffer); caches of the cache geometry described at nvs_store_kvcache. dtype bf16 or
+ * fp16. */
 int nvs_qk_norm_rope_store(const void* q, int64_t q_token_stride, const void* k, int64_t k_token_stride,
                            const void* v, int64_t v_token_stride, const int64_t* positions,
                            const void* q_norm_weight, const void* k_norm_weight, float eps,
                            const float* cos_sin_cache, int64_t cache_positions,
-                           const int32_t* slot_mapping, void* k_cache, void* v_cache, int64_t cache_slots,
+                           const int32_t* slot_mapping, void* k_cache, void* v_cache, int64_t cache_blocks,
+                           int64_t block_size, int64_t cache_block_stride, int64_t cache_token_stride,
+                           int64_t cache_head_stride,
                            void* q_out, int64_t q_out_token_stride, void* k_out, int64_t k_out_token_stride,
                            int64_t n_tokens, int n_heads, int n_kv_heads, int head_dim, int dtype, void* stream);
 

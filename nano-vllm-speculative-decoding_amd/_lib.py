@@ -35,9 +35,9 @@ _size_p = ctypes.POINTER(ctypes.c_size_t)
 SIGNATURES = {
     "nvs_abi_version": [],
     "nvs_last_error": [],
-    "nvs_store_kvcache": [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _i32, _i32, _p],
-    "nvs_qk_norm_rope_store": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _f32, _p, _i64, _p, _p, _p, _i64, _p, _i64,
-                               _p, _i64, _i64, _i32, _i32, _i32, _i32, _p],
+    "nvs_store_kvcache": [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i32, _i32, _i32, _p],
+    "nvs_qk_norm_rope_store": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _f32, _p, _i64, _p, _p, _p, _i64, _i64, _i64,
+                               _i64, _i64, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32, _p],
     "nvs_paged_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _size_p],
     "nvs_paged_attention": [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i32, _p, _p, _p, _i32,
                             _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _i64, _i64, _p,

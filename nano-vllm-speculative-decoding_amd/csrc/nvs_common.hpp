@@ -42,6 +42,22 @@ __host__ __device__ inline int dtype_size(int dtype) {
     }
 }
 
+// A paged K/V cache seen as [blocks, block_size, kv heads, head_dim] with element strides for the first three
+// dimensions (the head dimension is contiguous). Slot s is token s % block_size of block s / block_size. The
+// token-major layout [blocks, block_size, Hkv, D] has strides (block_size*Hkv*D, Hkv*D, D); the head-major layout
+// [blocks, Hkv, block_size, D], where every (block, head) is one contiguous run, has (Hkv*block_size*D, D,
+// block_size*D).
+struct CacheGeometry {
+    int64_t blocks;
+    int64_t block_size;
+    int64_t block_stride, token_stride, head_stride;
+    __host__ __device__ int64_t slots() const { return blocks * block_size; }
+    __host__ __device__ int64_t offset(int64_t slot, int head) const {
+        const int64_t b = slot / block_size;
+        return b * block_stride + (slot - b * block_size) * token_stride + head * head_stride;
+    }
+};
+
 // ---------------------------------------------------------------- device helpers
 
 // bf16 / f16 bit patterns -> fp32 (exact).

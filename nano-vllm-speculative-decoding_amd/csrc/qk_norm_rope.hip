@@ -40,8 +40,8 @@ struct NormRopeArgs {
     const float* cs;       // [n_cs, head_dim]: cos at [0, 64), sin at [64, 128)
     int64_t n_cs;
     const int32_t* slots;  // [T], < 0: not stored
-    int64_t cache_slots;
-    uint16_t* kc;          // [cache_slots, Hkv, head_dim]
+    nvs::CacheGeometry geo;  // of kc and vc (element strides)
+    uint16_t* kc;
     uint16_t* vc;
     uint16_t* qo;          // [T, Hq, head_dim]
     int64_t qo_ts;
@@ -76,12 +76,12 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void qk_norm_rope_store_kernel(
     const int l = threadIdx.x & 63;
     if (row >= a.hq + 2 * a.hkv) return;  // the whole wavefront
     const int32_t slot = a.slots != nullptr ? a.slots[t] : -1;
-    const bool store = slot >= 0 && slot < a.cache_slots;
+    const bool store = slot >= 0 && slot < a.geo.slots();
     if (row >= a.hq + a.hkv) {  // value head: a copy into the cache
         const int h = row - a.hq - a.hkv;
         if (store) {
             const uint16_t* src = a.v + t * a.v_ts + static_cast<int64_t>(h) * kHeadDim;
-            uint16_t* dst = a.vc + (static_cast<int64_t>(slot) * a.hkv + h) * kHeadDim;
+            uint16_t* dst = a.vc + a.geo.offset(slot, h);
             dst[l] = src[l];
             dst[l + kHalf] = src[l + kHalf];
         }
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void qk_norm_rope_store_kernel(
         dst[l + kHalf] = o2;
     }
     if (store) {
-        uint16_t* dst = a.kc + (static_cast<int64_t>(slot) * a.hkv + h) * kHeadDim;
+        uint16_t* dst = a.kc + a.geo.offset(slot, h);
         dst[l] = o1;
         dst[l + kHalf] = o2;
     }
@@ -138,7 +138,9 @@ extern "C" int nvs_qk_norm_rope_store(const void* q, int64_t q_token_stride, con
                                       const void* v, int64_t v_token_stride, const int64_t* positions,
                                       const void* q_norm_weight, const void* k_norm_weight, float eps,
                                       const float* cos_sin_cache, int64_t cache_positions,
-                                      const int32_t* slot_mapping, void* k_cache, void* v_cache, int64_t cache_slots,
+                                      const int32_t* slot_mapping, void* k_cache, void* v_cache,
+                                      int64_t cache_blocks, int64_t block_size, int64_t cache_block_stride,
+                                      int64_t cache_token_stride, int64_t cache_head_stride,
                                       void* q_out, int64_t q_out_token_stride, void* k_out,
                                       int64_t k_out_token_stride, int64_t n_tokens, int n_heads, int n_kv_heads,
                                       int head_dim, int dtype, void* stream) {
@@ -156,8 +158,11 @@ extern "C" int nvs_qk_norm_rope_store(const void* q, int64_t q_token_stride, con
     NVS_CHECK(n_heads == 0 || (q && q_out), NVS_ERR_INVALID, "qk_norm_rope_store: n_heads=%d needs q and q_out",
               n_heads);
     NVS_CHECK(cache_positions > 0, NVS_ERR_INVALID, "qk_norm_rope_store: empty cos_sin_cache");
-    NVS_CHECK(slot_mapping == nullptr || (k_cache && v_cache && cache_slots >= 0), NVS_ERR_INVALID,
-              "qk_norm_rope_store: slot_mapping needs k_cache, v_cache and cache_slots");
+    NVS_CHECK(slot_mapping == nullptr || (k_cache && v_cache && cache_blocks >= 0 && block_size > 0 &&
+                                          cache_block_stride >= 0 && cache_token_stride >= 0 &&
+                                          cache_head_stride >= 0),
+              NVS_ERR_INVALID, "qk_norm_rope_store: slot_mapping needs k_cache, v_cache and a cache geometry "
+              "(blocks >= 0, block_size > 0, strides >= 0)");
     NVS_CHECK(q_token_stride >= static_cast<int64_t>(n_heads) * head_dim &&
                   k_token_stride >= static_cast<int64_t>(n_kv_heads) * head_dim &&
                   v_token_stride >= static_cast<int64_t>(n_kv_heads) * head_dim &&
@@ -183,7 +188,8 @@ extern "C" int nvs_qk_norm_rope_store(const void* q, int64_t q_token_stride, con
     a.cs = cos_sin_cache;
     a.n_cs = cache_positions;
     a.slots = slot_mapping;
-    a.cache_slots = cache_slots;
+    a.geo = nvs::CacheGeometry{slot_mapping != nullptr ? cache_blocks : 0, block_size > 0 ? block_size : 1,
+                               cache_block_stride, cache_token_stride, cache_head_stride};
     a.kc = static_cast<uint16_t*>(k_cache);
     a.vc = static_cast<uint16_t*>(v_cache);
     a.qo = static_cast<uint16_t*>(q_out);

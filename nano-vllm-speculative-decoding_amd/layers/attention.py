@@ -20,31 +20,50 @@ from .. import _lib
 from ..utils.context import get_context
 
 
+def cache_geometry(k_cache: torch.Tensor, v_cache: torch.Tensor, num_kv_heads: int,
+                   head_dim: int) -> tuple[int, int, int, int, int]:
+    """(blocks, block_size, block_stride, token_stride, head_stride), in elements, of a K/V cache pair.
+
+    A 4-D cache [blocks, block_size, Hkv, D] may have any strides with a contiguous head dimension: the
+    token-major layout the reference allocates (model_runner.py:160), or a head-major view such as
+    torch.empty(blocks, Hkv, block_size, D).transpose(1, 2), in which each (block, head) is one contiguous run.
+    Other shapes must be contiguous [..., Hkv, D] and are one block of slots."""
+    if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must have one shape and one set of strides")
+    if tuple(k_cache.shape[-2:]) != (num_kv_heads, head_dim) or k_cache.stride(-1) != 1:
+        raise ValueError(f"the caches must be [..., {num_kv_heads}, {head_dim}] with a contiguous last dimension")
+    if k_cache.dim() == 4:
+        blocks, block_size = k_cache.shape[:2]
+        return blocks, block_size, k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    if not k_cache.is_contiguous():
+        raise ValueError("a cache that is not [blocks, block_size, Hkv, D] must be contiguous")
+    row = num_kv_heads * head_dim
+    slots = k_cache.numel() // row
+    return (1 if slots else 0), max(slots, 1), slots * row, row, head_dim
+
+
 def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                   slot_mapping: torch.Tensor) -> None:
     """Write token i's K/V rows into cache slot slot_mapping[i] (slot -1 = padding, skipped).
 
-    key/value: [N, Hkv, D] with contiguous rows (value may be a strided view of the fused qkv output);
-    k_cache/v_cache: [blocks, block_size, Hkv, D]; slot_mapping: [N] int32. Same preconditions as the reference
-    (attention.py:36-39)."""
+    key/value: [N, Hkv, D] with contiguous rows (value may be a strided view of the fused qkv output), the
+    reference's preconditions (attention.py:36-39); k_cache/v_cache: [blocks, block_size, Hkv, D], token-major as
+    the reference allocates them or head-major (cache_geometry); slot_mapping: [N] int32."""
     N, num_heads, head_dim = key.shape
-    D = num_heads * head_dim
     assert key.stride(-1) == 1 and value.stride(-1) == 1
     assert key.stride(1) == head_dim and value.stride(1) == head_dim
-    assert k_cache.stride(1) == D and v_cache.stride(1) == D
     assert slot_mapping.numel() == N
     _lib.require_device(key, value, k_cache, v_cache, slot_mapping)
     assert value.shape == key.shape and k_cache.dtype == key.dtype == value.dtype == v_cache.dtype
-    assert k_cache.is_contiguous() and v_cache.is_contiguous()
+    geo = cache_geometry(k_cache, v_cache, num_heads, head_dim)
     if slot_mapping.dtype != torch.int32:
         slot_mapping = slot_mapping.to(torch.int32)
     if not slot_mapping.is_contiguous():
         slot_mapping = slot_mapping.contiguous()
     lib = _lib.load()
     _lib.check(lib.nvs_store_kvcache(key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0),
-                                     k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // D,
-                                     slot_mapping.data_ptr(), N, num_heads, head_dim, _lib.dtype_code(key.dtype),
-                                     _lib.stream_of(key)),
+                                     k_cache.data_ptr(), v_cache.data_ptr(), *geo, slot_mapping.data_ptr(), N,
+                                     num_heads, head_dim, _lib.dtype_code(key.dtype), _lib.stream_of(key)),
                "store_kvcache")
 
 

@@ -15,6 +15,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
+from .attention import cache_geometry
 
 
 def rope_cos_sin_cache(head_size: int, max_position: int, base: float, device: torch.device) -> torch.Tensor:
@@ -44,7 +45,8 @@ def qk_norm_rope_store(positions: torch.Tensor, q: torch.Tensor | None, k: torch
     slot_mapping[t] (-1 = padding, skipped), and return the rotated q (written into q_out when given; q_out may be
     q itself). q=None runs the keys-only path and returns None. A None norm weight skips that norm (layers with a
     qkv bias). cos_sin_cache: the rotary table, [P, D] or the reference's [P, 1, D], fp32. k_out: optional
-    [T, Hkv, D] buffer for the rotated keys (the paged attention reads them from the cache instead)."""
+    [T, Hkv, D] buffer for the rotated keys (the paged attention reads them from the cache instead). The caches may
+    be token-major or head-major [blocks, block_size, Hkv, D] views (attention.cache_geometry)."""
     T, hkv, head_dim = k.shape
     hq = 0 if q is None else q.shape[1]
     _lib.require_device(positions, q, k, v, q_norm_weight, k_norm_weight, cos_sin_cache, k_cache, v_cache,
@@ -72,22 +74,19 @@ def qk_norm_rope_store(positions: torch.Tensor, q: torch.Tensor | None, k: torch
     if positions.dtype != torch.int64 or positions.numel() != T:
         raise ValueError("positions must be int64 with one entry per token")
     positions = positions.contiguous()
-    cache_slots = 0
+    geo = (0, 1, 0, 0, 0)
     if slot_mapping is not None:
         if k_cache is None or v_cache is None:
             raise ValueError("slot_mapping needs k_cache and v_cache")
         if slot_mapping.numel() != T:
             raise ValueError("slot_mapping needs one entry per token")
-        if not (k_cache.is_contiguous() and v_cache.is_contiguous()) or k_cache.shape != v_cache.shape \
-                or k_cache.shape[-2:] != (hkv, head_dim):
-            raise ValueError(f"k_cache / v_cache must be contiguous [..., {hkv}, {head_dim}] of one shape")
-        cache_slots = k_cache.numel() // (hkv * head_dim)
+        geo = cache_geometry(k_cache, v_cache, hkv, head_dim)
         slot_mapping = slot_mapping.to(torch.int32).contiguous()
     lib = _lib.load()
     _lib.check(lib.nvs_qk_norm_rope_store(_lib.ptr(q), q_ts, k.data_ptr(), k_ts, v.data_ptr(), v_ts,
                                           positions.data_ptr(), _lib.ptr(q_norm_weight), _lib.ptr(k_norm_weight),
                                           float(eps), cs.data_ptr(), cs.shape[0], _lib.ptr(slot_mapping),
-                                          _lib.ptr(k_cache), _lib.ptr(v_cache), cache_slots, _lib.ptr(q_out), qo_ts,
+                                          _lib.ptr(k_cache), _lib.ptr(v_cache), *geo, _lib.ptr(q_out), qo_ts,
                                           _lib.ptr(k_out), ko_ts, T, hq, hkv, head_dim, _lib.dtype_code(dtype),
                                           _lib.stream_of(k)),
                "qk_norm_rope_store")

@@ -32,6 +32,7 @@ from .layers import attention as nattn
 from .layers.activation import silu_and_mul
 from .layers.layernorm import rms_norm
 from .layers.qk_norm_rope import qk_norm_rope_store, rope_cos_sin_cache
+from .workloads import head_major_empty
 
 PAD_SLOT = -1
 
@@ -228,9 +229,13 @@ class Qwen3VerifyTarget:
                        for _ in range(s.num_layers)]
         self.norm = ones(s.hidden_size)
         self.lm_head = weight(s.vocab_size, s.hidden_size)
+        # Per layer a [num_blocks + 1, block_size, Hkv, D] view of head-major memory: the attention streams every
+        # (block, kv head) as one contiguous run (the reference's token-major layout works too, only slower).
         cache = (s.num_layers, num_blocks + 1, block_size, s.num_kv_heads, s.head_dim)
-        self.k_caches = torch.randn(cache, generator=g, device=self.device, dtype=dtype)
-        self.v_caches = torch.randn(cache, generator=g, device=self.device, dtype=dtype)
+        self.k_caches = head_major_empty(*cache, dtype=dtype, device=self.device)
+        self.v_caches = head_major_empty(*cache, dtype=dtype, device=self.device)
+        self.k_caches.normal_(generator=g)
+        self.v_caches.normal_(generator=g)
         self.k_caches[:, num_blocks].zero_()
         self.v_caches[:, num_blocks].zero_()
         self.cos_sin_cache = rope_cos_sin_cache(s.head_dim, s.max_position, s.rope_theta, self.device)

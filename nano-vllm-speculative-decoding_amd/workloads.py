@@ -65,6 +65,27 @@ class AttentionCase:
                 fields[name] = value.to(device)
         return AttentionCase(**fields)
 
+    def head_major(self) -> "AttentionCase":
+        """The same case with both caches stored head-major (head_major below)."""
+        fields = {name: getattr(self, name) for name in self.__dataclass_fields__}
+        fields["k_cache"] = head_major(self.k_cache)
+        fields["v_cache"] = head_major(self.v_cache)
+        return AttentionCase(**fields)
+
+
+def head_major_empty(*shape: int, dtype: torch.dtype, device=None) -> torch.Tensor:
+    """An uninitialised cache [..., blocks, block_size, Hkv, D] whose memory is [..., blocks, Hkv, block_size, D]:
+    every (block, kv head) is one contiguous run of block_size * D elements."""
+    *lead, block_size, hkv, d = shape
+    return torch.empty(*lead, hkv, block_size, d, dtype=dtype, device=device).transpose(-3, -2)
+
+
+def head_major(cache: torch.Tensor) -> torch.Tensor:
+    """A head-major copy of a [..., blocks, block_size, Hkv, D] cache, equal to it element for element."""
+    out = head_major_empty(*cache.shape, dtype=cache.dtype, device=cache.device)
+    out.copy_(cache)
+    return out
+
 
 def verify_attention_case(q_lens: list[int], k_lens: list[int], num_heads: int, num_kv_heads: int, head_dim: int,
                           block_size: int = 256, dtype: torch.dtype = torch.bfloat16, pad_tokens_to: int = 8,

@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version_and_empty_error(lib):
-    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 6
     assert isinstance(lib.nvs_last_error(), bytes)
 
 
@@ -103,17 +103,24 @@ def test_sampler_rejects_bad_arguments_without_launching(lib):
 
 
 def test_store_kvcache_rejects_bad_arguments(lib):
-    assert lib.nvs_store_kvcache(1 << 20, 1024, 1 << 20, 1024, 1 << 21, 1 << 22, 100, 1 << 23, 4, 8, 128, 7,
-                                 None) == _lib.NVS_ERR_INVALID
-    assert lib.nvs_store_kvcache(1 << 20, 512, 1 << 20, 1024, 1 << 21, 1 << 22, 100, 1 << 23, 4, 8, 128,
-                                 _lib.DTYPE_BF16, None) == _lib.NVS_ERR_INVALID
-    assert lib.nvs_store_kvcache(None, 0, None, 0, None, None, 0, None, 0, 8, 128, _lib.DTYPE_BF16, None) == 0
+    nhd = (100, 256, 256 * 1024, 1024, 128)   # blocks, block size, block / token / head strides
+    assert lib.nvs_store_kvcache(1 << 20, 1024, 1 << 20, 1024, 1 << 21, 1 << 22, *nhd, 1 << 23, 4, 8, 128, 7,
+                                 None) == _lib.NVS_ERR_INVALID        # unknown dtype
+    assert lib.nvs_store_kvcache(1 << 20, 512, 1 << 20, 1024, 1 << 21, 1 << 22, *nhd, 1 << 23, 4, 8, 128,
+                                 _lib.DTYPE_BF16, None) == _lib.NVS_ERR_INVALID   # key rows shorter than 8 x 128
+    assert lib.nvs_store_kvcache(1 << 20, 1024, 1 << 20, 1024, 1 << 21, 1 << 22, 100, 0, 1, 1, 1, 1 << 23, 4, 8,
+                                 128, _lib.DTYPE_BF16, None) == _lib.NVS_ERR_INVALID   # block size 0
+    assert lib.nvs_store_kvcache(1 << 20, 1024, 1 << 20, 1024, 1 << 21, 1 << 22, 100, 256, -1, 1024, 128, 1 << 23,
+                                 4, 8, 128, _lib.DTYPE_BF16, None) == _lib.NVS_ERR_INVALID   # negative stride
+    assert lib.nvs_store_kvcache(None, 0, None, 0, None, None, 0, 256, 0, 0, 0, None, 0, 8, 128, _lib.DTYPE_BF16,
+                                 None) == 0
 
 
 def test_qk_norm_rope_store_rejects_bad_arguments(lib):
     def call(**over):
         a = dict(q=1 << 20, q_ts=6144, k=1 << 21, k_ts=6144, v=1 << 22, v_ts=6144, pos=1 << 23, qw=None, kw=None,
-                 eps=1e-6, cs=1 << 24, n_cs=4096, slots=None, kc=None, vc=None, cache_slots=0, qo=1 << 25,
+                 eps=1e-6, cs=1 << 24, n_cs=4096, slots=None, kc=None, vc=None, blocks=0, block_size=256,
+                 bs=256 * 1024, ts=1024, hs=128, qo=1 << 25,
                  qo_ts=4096, ko=None, ko_ts=0, T=4, hq=32, hkv=8, d=128, dtype=_lib.DTYPE_BF16, stream=None)
         a.update(over)
         return lib.nvs_qk_norm_rope_store(*a.values())
@@ -122,6 +129,8 @@ def test_qk_norm_rope_store_rejects_bad_arguments(lib):
     assert call(q=None) == _lib.NVS_ERR_INVALID            # query heads without q
     assert call(k_ts=512) == _lib.NVS_ERR_INVALID          # shorter than 8 heads x 128
     assert call(slots=1 << 26) == _lib.NVS_ERR_INVALID     # slots without caches
+    assert call(slots=1 << 26, kc=1 << 27, vc=1 << 28, blocks=4, block_size=0) == _lib.NVS_ERR_INVALID
+    assert call(slots=1 << 26, kc=1 << 27, vc=1 << 28, blocks=4, hs=-128) == _lib.NVS_ERR_INVALID
     assert call(n_cs=0) == _lib.NVS_ERR_INVALID
     assert call(T=0) == _lib.NVS_OK                        # nothing to do, nothing launched
 

@@ -209,9 +209,10 @@ def test_store_kvcache_bit_exact_strided_value_and_padding(device):
     assert torch.equal(gk.cpu(), want_k) and torch.equal(gv.cpu(), want_v)
 
 
+@pytest.mark.parametrize("layout", ["token_major", "head_major"])
 @pytest.mark.parametrize("dtype, head_dim", [(torch.float32, 64), (torch.float16, 128), (torch.bfloat16, 4)])
-def test_store_kvcache_other_dtypes_and_unaligned_rows(device, dtype, head_dim):
-    log_case(f"store_kvcache {dtype} head_dim {head_dim}")
+def test_store_kvcache_other_dtypes_and_unaligned_rows(device, dtype, head_dim, layout):
+    log_case(f"store_kvcache {dtype} head_dim {head_dim} {layout}")
     N, hkv, bs, blocks = 11, 2, 32, 3
     key = torch.randn(N, hkv, head_dim).to(dtype)
     value = torch.randn(N, hkv, head_dim).to(dtype)
@@ -219,7 +220,55 @@ def test_store_kvcache_other_dtypes_and_unaligned_rows(device, dtype, head_dim):
     want_k = torch.zeros(blocks, bs, hkv, head_dim, dtype=dtype)
     want_v = torch.zeros_like(want_k)
     ref.store_kvcache(key, value, want_k, want_v, slots)
-    gk, gv = torch.zeros_like(want_k, device=device), torch.zeros_like(want_v, device=device)
+    if layout == "head_major":
+        gk = wl.head_major_empty(*want_k.shape, dtype=dtype, device=device).zero_()
+        gv = wl.head_major_empty(*want_v.shape, dtype=dtype, device=device).zero_()
+    else:
+        gk, gv = torch.zeros_like(want_k, device=device), torch.zeros_like(want_v, device=device)
     nattn.store_kvcache(key.to(device), value.to(device), gk, gv, slots.to(device))
     torch.cuda.synchronize()
     assert torch.equal(gk.cpu(), want_k) and torch.equal(gv.cpu(), want_v)
+
+
+def test_store_kvcache_head_major_strided_value(device):
+    log_case("store_kvcache into head-major caches, strided value, padding slots")
+    N, hkv, d, bs, blocks = 37, 8, 128, 256, 5
+    gen = torch.Generator().manual_seed(4)
+    qkv = torch.randn(N, (32 + 2 * hkv) * d, generator=gen).to(torch.bfloat16)
+    slots = torch.randperm(blocks * bs, generator=gen)[:N].to(torch.int32)
+    slots[[0, 17]] = -1
+    want_k = torch.zeros(blocks, bs, hkv, d, dtype=torch.bfloat16)
+    want_v = torch.zeros_like(want_k)
+    ref.store_kvcache(qkv[:, 32 * d:(32 + hkv) * d].reshape(N, hkv, d), qkv[:, (32 + hkv) * d:].reshape(N, hkv, d),
+                      want_k, want_v, slots)
+    gk = wl.head_major_empty(blocks, bs, hkv, d, dtype=torch.bfloat16, device=device).zero_()
+    gv = wl.head_major_empty(blocks, bs, hkv, d, dtype=torch.bfloat16, device=device).zero_()
+    assert gk.stride() == (hkv * bs * d, d, bs * d, 1)
+    qkv_d = qkv.to(device)
+    nattn.store_kvcache(qkv_d[:, 32 * d:(32 + hkv) * d].view(N, hkv, d), qkv_d[:, (32 + hkv) * d:].view(N, hkv, d),
+                        gk, gv, slots.to(device))
+    torch.cuda.synchronize()
+    assert torch.equal(gk.cpu(), want_k) and torch.equal(gv.cpu(), want_v)
+
+
+@pytest.mark.parametrize("shape", ["c2_split", "c3", "draft_block"])
+def test_head_major_cache_gives_the_token_major_result(device, shape):
+    """The kernel reads a cache through its strides: head-major memory gives bit for bit the token-major result."""
+    log_case(f"attention head-major vs token-major {shape}")
+    if shape == "draft_block":
+        c = wl.verify_attention_case([7] * 16, [900 + 37 * i for i in range(16)], 32, 8, 128, pad_tokens_to=1)
+    else:
+        c = wl.config_c2() if shape == "c2_split" else wl.config_c3()
+    g, h = c.to(device), c.head_major().to(device)
+    assert h.k_cache.stride(1) == 128 and torch.equal(h.k_cache, g.k_cache)
+    if shape == "draft_block":
+        ctx = torch.tensor(c.k_lens, dtype=torch.int32, device=device)
+        outs = [nattn._paged_attention(x.q, x.k_cache, x.v_cache, x.block_tables, None, None, ctx, 7, 16, 7, 4096,
+                                       x.scale, False) for x in (g, h)]
+    else:
+        outs = [nattn._paged_attention(x.q, x.k_cache, x.v_cache, x.block_tables, x.cu_seqlens_q, x.cu_seqlens_k,
+                                       None, 0, len(c.q_lens), x.max_seqlen_q, 4096, x.scale, True) for x in (g, h)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    if shape == "c2_split":
+        check(outs[1].float().cpu(), c)

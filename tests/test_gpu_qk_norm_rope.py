@@ -42,10 +42,13 @@ def close_to_oracle(got: torch.Tensor, want: torch.Tensor, what: str, rotated: t
     assert same >= 0.99, f"{what}: only {100 * same:.2f}% bit-identical"
 
 
-def run_case(case: wl.QkRopeCase, device, keys_only=False, norms=True, in_place=False):
+def run_case(case: wl.QkRopeCase, device, keys_only=False, norms=True, in_place=False, head_major=False):
     g = case.to(device)
     q, k, v = g.split()
-    kc, vc = g.k_cache.clone(), g.v_cache.clone()
+    if head_major:
+        kc, vc = wl.head_major(g.k_cache), wl.head_major(g.v_cache)
+    else:
+        kc, vc = g.k_cache.clone(), g.v_cache.clone()
     qw = g.q_norm_weight if norms else None
     kw = g.k_norm_weight if norms else None
     q_in = None if keys_only else q
@@ -68,8 +71,8 @@ def check_caches(case, kc, vc, refs):
     kc_ref, vc_ref, k_norm = refs
     live = case.slot_mapping >= 0
     slots = case.slot_mapping[live].long()
-    flat_k, flat_v = kc.cpu().view(-1, case.num_kv_heads, case.head_dim), vc.cpu().view(-1, case.num_kv_heads,
-                                                                                       case.head_dim)
+    flat_k = kc.cpu().contiguous().view(-1, case.num_kv_heads, case.head_dim)   # logical [slot, head, dim] order
+    flat_v = vc.cpu().contiguous().view(-1, case.num_kv_heads, case.head_dim)
     ref_k, ref_v = kc_ref.view_as(flat_k), vc_ref.view_as(flat_v)
     close_to_oracle(flat_k[slots], ref_k[slots], "k in cache", k_norm[live])
     assert torch.equal(flat_v[slots], ref_v[slots]), "v copies must be bit-exact"
@@ -83,6 +86,17 @@ def test_qwen3_8b_shape(device, num_tokens):
     log_case(f"qk norm rope store qwen3-8b T={num_tokens}")
     case = wl.qk_rope_case(num_tokens, num_padding=min(8, num_tokens - 1))
     out, kc, vc, q_ref, refs, q_norm = run_case(case, device)
+    close_to_oracle(out, q_ref, "q", q_norm)
+    check_caches(case, kc, vc, refs)
+
+
+def test_head_major_cache(device):
+    """Caches stored head-major ([blocks, Hkv, block_size, D] memory behind the [blocks, block_size, Hkv, D] view):
+    the same values land in the same logical slots, and nothing else is written."""
+    log_case("qk norm rope store into head-major caches, qwen3-8b T=296")
+    case = wl.qk_rope_case(296, num_padding=8, seed=6)
+    out, kc, vc, q_ref, refs, q_norm = run_case(case, device, head_major=True)
+    assert kc.stride(1) == case.head_dim and not kc.is_contiguous()
     close_to_oracle(out, q_ref, "q", q_norm)
     check_caches(case, kc, vc, refs)
 

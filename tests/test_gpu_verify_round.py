@@ -128,7 +128,9 @@ def rel_l2(got, want):
 def test_forward_matches_the_cpu_oracle(device):
     log_case("verify forward, 2 small Qwen3 layers, 6 rows")
     batch, target, ids = small_setup(device)
-    k0, v0 = target.k_caches.cpu(), target.v_caches.cpu()
+    # the target's caches are head-major; the CPU copies are token-major, equal element for element
+    assert target.k_caches.stride(-2) == SMALL.head_dim * 256 and not target.k_caches.is_contiguous()
+    k0, v0 = target.k_caches.cpu().contiguous(), target.v_caches.cpu().contiguous()
     graphs = vr.VerifyGraphs(target, max_batch_size=8, query_len=8, max_model_len=1024)
     got = graphs.run_eager(batch, ids.to(device)).clone()
     torch.cuda.synchronize()
@@ -137,7 +139,7 @@ def test_forward_matches_the_cpu_oracle(device):
     print(f"hidden: relative L2 error {err:.2e}")
     assert err <= 2e-2
     for name, mine, ref in (("keys", target.k_caches, k0), ("values", target.v_caches, v0)):
-        flat_m = mine.cpu().view(SMALL.num_layers, -1, SMALL.num_kv_heads, SMALL.head_dim)
+        flat_m = mine.cpu().contiguous().view(SMALL.num_layers, -1, SMALL.num_kv_heads, SMALL.head_dim)
         flat_r = ref.view_as(flat_m)
         live = slots[slots >= 0].long()
         err = rel_l2(flat_m[:, live], flat_r[:, live])
