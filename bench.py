@@ -240,6 +240,81 @@ def draft_block_bench(args, dev):
             "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": b}
 
 
+def graph_timed(fn, args, reps: int = 10) -> float:
+    """ms per call of fn as it runs inside a verify graph: reps calls captured in one HIP graph (after one eager
+    call on a side stream), the graph replayed and timed by time_gpu."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    return time_gpu(graph.replay, max(10, args.steps // 4), 3) / reps
+
+
+def rows_bench(args, dev):
+    """The hot path's other entry points on their own, each timed per call inside a HIP graph (graph_timed):
+    the KV store of a batch-64 verify layer (296 tokens, 8 kv heads, value a strided view of the fused qkv, head-
+    major cache), and over 64 rows x 8 positions x 151,936 fp32 logits ~N(0, 3^2) with top-k 64: probs_from_logits,
+    truncate_logits, the race of sample() over [64, V], and accept_random on dense p and q (the unfused path)."""
+    import torch
+
+    import nvs_amd.workloads as wl
+    from nvs_amd.layers import attention as nattn
+    from nvs_amd.layers import spec_sampler as ns
+    gen = torch.Generator(device=dev).manual_seed(11)
+    rows = {}
+
+    def report(name, ms, nbytes, what):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows[name] = {"us": round(ms * 1e3, 2), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                      "bytes": nbytes, "bytes_are": what}
+        log(f"[bench] {name}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s = {100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
+
+    # a1: store_kvcache, 296 tokens into a head-major cache of 786 blocks
+    n_tok, hkv, d, blocks = 296, 8, 128, 786
+    qkv = torch.randn(n_tok, (32 + 2 * hkv) * d, generator=gen, device=dev).to(torch.bfloat16)
+    key = qkv[:, 32 * d:(32 + hkv) * d].view(n_tok, hkv, d)
+    value = qkv[:, (32 + hkv) * d:].view(n_tok, hkv, d)
+    kc = wl.head_major_empty(blocks, 256, hkv, d, dtype=torch.bfloat16, device=dev).zero_()
+    vc = wl.head_major_empty(blocks, 256, hkv, d, dtype=torch.bfloat16, device=dev).zero_()
+    slots = torch.randperm(blocks * 256, generator=gen, device=dev)[:n_tok].to(torch.int32)
+    ms = graph_timed(lambda: nattn.store_kvcache(key, value, kc, vc, slots), args)
+    report("a1_store_kvcache", ms, 2 * 2 * n_tok * hkv * d * 2, "K and V rows read and written")
+    del kc, vc
+
+    # a5: probs_from_logits and truncate_logits over [64, 8, V] fp32
+    B, k, V = 64, 7, 151936
+    logits = (torch.randn(B, k + 1, V, generator=gen, device=dev) * 3).contiguous()
+    st = ns.SamplingTensors(torch.ones(B, device=dev), torch.full((B,), 64, dtype=torch.int64, device=dev),
+                            torch.ones(B, device=dev), 64, False, True)
+    ms = graph_timed(lambda: ns.probs_from_logits(logits, st), args)
+    report("a5_probs_from_logits", ms, 2 * logits.numel() * 4, "logits read, probabilities written (fp32)")
+    ms = graph_timed(lambda: ns.truncate_logits(logits, st), args)
+    report("a5_truncate_logits", ms, 2 * logits.numel() * 4, "scaled logits read, truncated logits written")
+
+    # a6: the race of sample() over [64, V]
+    p = ns.probs_from_logits(logits, st)
+    noise = torch.empty(B, V, device=dev).exponential_(1.0, generator=gen).clamp_min_(1e-10)
+    weights = p[:, 0].contiguous()
+    ms = graph_timed(lambda: ns.race(weights, noise), args)
+    report("a6_race", ms, 2 * B * V * 4, "weights and noise read")
+
+    # a7: accept_random on dense p [512, V] and q [64, 7, V]
+    q = torch.softmax(torch.randn(B, k, V, generator=gen, device=dev) * 3, dim=-1)
+    drafts = torch.randint(0, V, (B, k), generator=gen, device=dev)
+    uniforms = torch.rand(B, k, generator=gen, device=dev)
+    ms = graph_timed(lambda: ns.accept_random_with_draws(p, q, drafts, None, uniforms, noise), args)
+    report("a7_accept_random_dense", ms, 3 * B * V * 4, "each row's race reads its p row, q row and noise row")
+    del logits, p, q
+    torch.cuda.empty_cache()
+    return rows
+
+
 def qk_rope_bench(args, dev):
     """The fused q/k RMSNorm + rotary + KV store of one batch-64 verify layer (296 tokens, 32/8 heads), against
     the same sequence as separate torch ops on the GPU (norm q, norm k, rotate both, index the caches)."""
@@ -529,6 +604,7 @@ def main():
              "qk_norm_rope_store": qk_rope_bench(args, dev)}
     if args.sampler == "on":
         extra["sampler"] = sampler_bench(args, dev)
+        extra["rows"] = rows_bench(args, dev)
         extra["markov_rows"] = markov_bench(args, dev)
     if args.verify_round == "on":
         extra["verify_round"] = verify_round_bench(args, dev)

@@ -9,7 +9,9 @@
 //   The query tile packs the GQA query heads of kv head g and all query positions of the row into 32 "packed rows"
 //   n = qpos * group + hg, so every K/V byte of the row's kv head is read from HBM once for all of them
 //   (Qwen3-8B: group 4 x 8 verify positions = 32 rows).
-//   The key range [0, Lk) is cut into splits of split_tokens keys; each wave of the workgroup takes every 4th
+//   The key range [0, Lk) is cut into at most n_splits splits of equal size, whole 32-key chunks and at least
+//   split_tokens keys each, sized from the row's own Lk on the device (the grid depends only on host integers, so
+//   a captured graph serves every batch); each wave of the workgroup takes every 4th
 //   32-key chunk of its split and keeps its own online-softmax state. The 4 waves are merged in LDS
 //   (deterministic order); a row with a single split writes bf16 output directly, otherwise each split writes an
 //   fp32 partial (O, max, sum) and attn_combine_kernel merges them with the log-sum-exp rule.
@@ -42,7 +44,7 @@ constexpr int kTileRows = 32;    // packed query rows per tile
 constexpr int kChunk = 32;       // keys per MFMA chunk
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kSplitQuantum = kChunk * kWaves;  // split_tokens is a multiple of this
+constexpr int kSplitQuantum = kChunk * kWaves;  // the planned split size is a multiple of this
 // Wave-private K and V tiles in LDS: [32 keys][128 dims] bf16 each, rows padded from 256 to 272 B (68 dwords,
 // 4 banks apart) so that the staging stores (8 lanes along one row), the K operand reads (32 rows at one column)
 // and the transposed V reads (one row per half-wave, 32 consecutive dims) are all free of bank conflicts.
@@ -75,7 +77,7 @@ struct AttnArgs {
     int64_t o_ts, o_hs;
     float* part_o;   // [units, n_splits, 32, 128]
     float* part_ml;  // [units, n_splits, 32, 2]
-    int n_splits, split_tokens, q_tiles;
+    int n_splits, split_tokens, q_tiles;   // split_tokens: the smallest split of a row with several
 };
 
 struct RowInfo {
@@ -96,10 +98,18 @@ __device__ __forceinline__ RowInfo row_info(const AttnArgs& a, int r) {
     return ri;
 }
 
-// Splits holding keys of a row with lk keys (at least one, so a row without keys still writes zeros); never more
-// than the grid has, so a length above max_seqlen_k cannot send the combine past the partial buffers.
-__device__ __forceinline__ int active_splits(int lk, int split_tokens, int n_splits) {
-    return lk > 0 ? min((lk + split_tokens - 1) / split_tokens, n_splits) : 1;
+// Keys per split of a row with lk keys: the row spread evenly over the grid's n_splits splits, rounded up to whole
+// 32-key chunks (a chunk never straddles a page), at least min_tokens. ceil(lk / that) <= n_splits, so a length
+// above max_seqlen_k cannot send the combine past the partial buffers.
+__device__ __forceinline__ int row_split_tokens(int lk, int min_tokens, int n_splits) {
+    if (n_splits <= 1) return max(lk, 1);
+    const int even = (lk + n_splits - 1) / n_splits;
+    return max((even + kChunk - 1) / kChunk * kChunk, min_tokens);
+}
+
+// Splits holding keys of a row (at least one, so a row without keys still writes zeros).
+__device__ __forceinline__ int active_splits(int lk, int split_len) {
+    return lk > 0 ? (lk + split_len - 1) / split_len : 1;
 }
 
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
@@ -117,10 +127,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
     const RowInfo ri = row_info(a, r);
     const int n_base = qt * kTileRows;
     if (ri.lq <= 0 || n_base >= a.group * ri.lq) return;
-    const int n_act = active_splits(ri.lk, a.split_tokens, a.n_splits);
+    const int split_len = row_split_tokens(ri.lk, a.split_tokens, a.n_splits);
+    const int n_act = active_splits(ri.lk, split_len);
     if (s >= n_act) return;
-    const int k0 = s * a.split_tokens;
-    const int k1 = min(k0 + a.split_tokens, ri.lk);
+    const int k0 = s * split_len;
+    const int k1 = min(k0 + split_len, ri.lk);
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -360,7 +371,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     const RowInfo ri = row_info(a, r);
     const int n_base = qt * kTileRows;
     if (ri.lq <= 0 || n_base >= a.group * ri.lq) return;
-    const int n_act = active_splits(ri.lk, a.split_tokens, a.n_splits);
+    const int n_act = active_splits(ri.lk, row_split_tokens(ri.lk, a.split_tokens, a.n_splits));
     if (n_act <= 1) return;
     const int64_t unit = (static_cast<int64_t>(r) * a.n_kv + g) * a.q_tiles + qt;
     for (int e = threadIdx.x; e < kTileRows * kHeadDim / 4; e += blockDim.x) {
@@ -425,9 +436,11 @@ SplitPlan plan_splits(int n_rows, int n_heads, int n_kv_heads, int max_seqlen_q,
         if (v > 0) min_ts = v;
     }
     ts = (ts + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum;
-    min_ts = (min_ts + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum;
+    min_ts = (min_ts + kChunk - 1) / kChunk * kChunk;
     if (ts < min_ts) ts = min_ts;
-    p.split_tokens = static_cast<int>(ts);
+    // The grid has n_splits splits per unit, from max_seqlen_k; each row spreads its own keys over them on the
+    // device, at least split_tokens per split.
+    p.split_tokens = static_cast<int>(min_ts);
     p.n_splits = static_cast<int>((max_k + ts - 1) / ts);
     if (p.n_splits < 1) p.n_splits = 1;
     p.workspace = 0;

@@ -2043,6 +2043,32 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         return;
     } else if constexpr (MODE == kModeProbs || MODE == kModeTruncate) {
         float* orow = a.out + t * a.out_stride;
+        if (!rs.dense && kept_source != kKeptInRow && theta_key != 0u) {
+            // Every kept value (key >= theta_key > 0: NaN is never kept) is in LDS, in the short list or the lane
+            // lists. The row is filled with the value of an element outside the kept set (probability 0, logit
+            // -inf) with 16-byte stores, then the kept values are written over it: the logits are not read again.
+            const float fill = MODE == kModeProbs ? 0.f : -INFINITY;
+            const int64_t n4 = (reinterpret_cast<uintptr_t>(orow) & 15u) == 0 ? a.vocab / 4 : 0;
+            const float4 f4 = make_float4(fill, fill, fill, fill);
+            for (int64_t i = threadIdx.x; i < n4; i += kSelThreads) reinterpret_cast<float4*>(orow)[i] = f4;
+            for (int64_t e = n4 * 4 + threadIdx.x; e < a.vocab; e += kSelThreads) orow[e] = fill;
+            __syncthreads();   // the fill stores are performed before any kept value is written over them
+            const bool short_list = kept_source == kKeptInShortList;
+            const int n = short_list ? sh.count : min(sh.count, kCap);
+            for (int c = threadIdx.x; c < n; c += kSelThreads) {
+                const uint32_t key = short_list ? sh.sortbuf[c] : sh.ckey[c];
+                if (key < theta_key) continue;
+                const int64_t e = short_list ? static_cast<int64_t>(sh.sortbuf[kSelWaves * 64 + c])
+                                             : static_cast<int64_t>(sh.cidx[c]);
+                const float s = nvs::key_float(key);
+                if constexpr (MODE == kModeProbs) {
+                    orow[e] = expf(s - mu) / rs.z;
+                } else {
+                    orow[e] = s;
+                }
+            }
+            return;
+        }
         for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
             float v[kVpt];
             load_vals<DT, VEC>(row, e0, a.vocab, v);

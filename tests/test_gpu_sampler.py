@@ -116,7 +116,7 @@ def probs_params(n, vocab, top_k, top_p, temp, seed, dtype=torch.float32, sigma=
     ("bf16_ties", [64, 50], [1.0, 0.8], [1.0], torch.bfloat16),
     ("topk1000", [1000, 700], [1.0, 0.95], [1.0], torch.float32),
 ])
-@pytest.mark.parametrize("vocab", [5000, 151936])
+@pytest.mark.parametrize("vocab", [4099, 5000, 151936])   # 4099: rows that are not 16-byte aligned
 def test_probs_and_truncation_match_the_oracle(device, name, top_k, top_p, temp, dtype, vocab):
     log_case(f"probs_from_logits {name} V={vocab}")
     logits, rows = probs_params(16, vocab, top_k, top_p, temp, seed=len(name) + vocab)
