@@ -34,7 +34,8 @@ constexpr int kLaneCap = 16;                   // candidate slots per lane durin
 constexpr int kWaveSlots = kLaneCap * 64;      // a wave's slots: slot s of lane l at s * 64 + l
 constexpr int kCap = kSelWaves * kWaveSlots;   // LDS candidate capacity (8192)
 constexpr int kMaxTopK = 1024;
-constexpr int kRaceChunk = 16384;              // vocabulary chunk of the dense race kernels
+constexpr int kRaceChunk = 8192;               // vocabulary chunk of the dense race kernels (256 threads)
+constexpr int kRacePer = kRaceChunk / 4 / 256;  // 16-byte pieces per thread and array
 
 enum Mode { kModeAccept = 0, kModeProbs = 1, kModeTruncate = 2, kModeMarkov = 3 };
 
@@ -2198,28 +2199,59 @@ struct RaceArgs {
 
 // Accepted prefix of row b over dense p (accept_random_varlen's gathers, spec_sampler.py:134-143).
 __device__ int64_t accepted_prefix(const RaceArgs& a, int64_t b, int64_t start, int64_t L) {
+    // Draft n is tested only when every draft before it was accepted (spec_sampler.py:136-141): the prefix is the
+    // number of leading accepted drafts among the first lim = min(L - 1, k, n_pos - start). Wave 0 tests them all
+    // at once, one lane per draft (two dependent loads: the draft, then p and q at it), and counts the leading
+    // accepted lanes; rows with more than 64 drafts are walked in steps of 64.
     __shared__ int64_t n_sh;
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 64) {
+        const int64_t lim = min(min(L - 1, static_cast<int64_t>(a.k)), a.n_pos - start);
         int64_t n = 0;
-        while (n < L - 1 && n < a.k && start + n < a.n_pos) {
-            const int64_t d = a.drafts[b * a.k + n];
-            if (d < 0 || d >= a.vocab) break;  // an out-of-vocabulary draft is never accepted
-            const float pd = a.p[(start + n) * a.p_stride + d];
-            const float qd = a.q[(b * a.k + n) * a.vocab + d];
-            if (!(a.uniforms[b * a.k + n] * qd < pd)) break;
-            ++n;
+        for (int64_t j0 = 0; j0 < lim; j0 += 64) {
+            const int64_t j = j0 + threadIdx.x;
+            bool acc = false;
+            if (j < lim) {
+                const int64_t d = a.drafts[b * a.k + j];
+                const float u = a.uniforms[b * a.k + j];
+                if (d >= 0 && d < a.vocab) {   // an out-of-vocabulary draft is never accepted
+                    const float pd = a.p[(start + j) * a.p_stride + d];
+                    const float qd = a.q[(b * a.k + j) * a.vocab + d];
+                    acc = u * qd < pd;
+                }
+            }
+            const uint64_t rejected = ~__ballot(acc);
+            if (rejected != 0ull) {
+                n = j0 + __builtin_ctzll(rejected);
+                break;
+            }
+            n = j0 + 64;
         }
-        n_sh = n;
+        if (threadIdx.x == 0) n_sh = min(n, max(lim, int64_t{0}));
     }
     __syncthreads();
     return n_sh;
 }
 
-template <bool kAccept>
+// One workgroup = (row r, chunk c of kRaceChunk elements): the best (score, -index) key of the chunk. VEC (every
+// row 16-byte aligned, vocab a multiple of 4): each thread takes kRacePer 16-byte pieces of each array, all loads
+// issued before any is used, the noise first (it does not depend on the accepted prefix), from addresses clamped
+// into the chunk; pieces past the chunk are loaded but not scored.
+template <bool kAccept, bool VEC>
 __global__ __launch_bounds__(256) void race_chunk_kernel(RaceArgs a) {
     __shared__ uint64_t red[4];
     const int64_t r = blockIdx.x;   // rows on x (up to 2^31), vocabulary chunks on y
     const int c = blockIdx.y;
+    const float* erow = a.noise + r * a.noise_stride;
+    const int64_t i0 = static_cast<int64_t>(c) * kRaceChunk;
+    const int64_t i1 = min(i0 + kRaceChunk, a.vocab);
+    float4 ev[kRacePer];
+    if constexpr (VEC) {
+#pragma unroll
+        for (int m = 0; m < kRacePer; ++m) {
+            const int64_t j = min((i0 >> 2) + threadIdx.x + 256 * m, (i1 >> 2) - 1);
+            ev[m] = reinterpret_cast<const float4*>(erow)[j];
+        }
+    }
     const float* wrow;
     const float* qrow = nullptr;
     bool bonus = true;
@@ -2234,17 +2266,43 @@ __global__ __launch_bounds__(256) void race_chunk_kernel(RaceArgs a) {
     } else {
         wrow = a.p + r * a.p_stride;
     }
-    const float* erow = a.noise + r * a.noise_stride;
-    const int64_t i0 = static_cast<int64_t>(c) * kRaceChunk;
-    const int64_t i1 = min(i0 + kRaceChunk, a.vocab);
+    auto key_of = [](float w, float e, int64_t i) {
+        const float score = w / e;
+        return (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+               static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
+    };
     uint64_t best = 0;
-    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
-        float w = wrow[i];
-        if (kAccept && !bonus) w = fmaxf(w - qrow[i], 0.f);
-        const float score = w / erow[i];
-        const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
-                             static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
-        best = best > k64 ? best : k64;
+    if constexpr (VEC) {
+        float4 wv[kRacePer], qv[kRacePer];
+#pragma unroll
+        for (int m = 0; m < kRacePer; ++m) {
+            const int64_t j = min((i0 >> 2) + threadIdx.x + 256 * m, (i1 >> 2) - 1);
+            wv[m] = reinterpret_cast<const float4*>(wrow)[j];
+            // a bonus row has no q; its pieces are then the w row's again (never used)
+            if constexpr (kAccept) qv[m] = reinterpret_cast<const float4*>(!bonus ? qrow : wrow)[j];
+        }
+#pragma unroll
+        for (int m = 0; m < kRacePer; ++m) {
+            const int64_t j = (i0 >> 2) + threadIdx.x + 256 * m;
+            if (j >= (i1 >> 2)) continue;
+            const float w4[4] = {wv[m].x, wv[m].y, wv[m].z, wv[m].w};
+            const float q4[4] = {kAccept ? qv[m].x : 0.f, kAccept ? qv[m].y : 0.f, kAccept ? qv[m].z : 0.f,
+                                 kAccept ? qv[m].w : 0.f};
+            const float e4[4] = {ev[m].x, ev[m].y, ev[m].z, ev[m].w};
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const float w = (kAccept && !bonus) ? fmaxf(w4[l] - q4[l], 0.f) : w4[l];
+                const uint64_t k64 = key_of(w, e4[l], 4 * j + l);
+                best = best > k64 ? best : k64;
+            }
+        }
+    } else {
+        for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+            float w = wrow[i];
+            if (kAccept && !bonus) w = fmaxf(w - qrow[i], 0.f);
+            const uint64_t k64 = key_of(w, erow[i], i);
+            best = best > k64 ? best : k64;
+        }
     }
     best = wave_max_u64(best);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
@@ -2625,7 +2683,13 @@ extern "C" int nvs_race(const float* weights, int64_t weights_row_stride, const 
     a.partial = static_cast<uint64_t*>(workspace);
     a.out = out;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(race_chunk_kernel<false>, dim3(n_rows, a.n_chunks), dim3(256), 0, s, a);
+    const bool vec = vocab % 4 == 0 && nvs::aligned16(weights) && nvs::aligned16(noise) &&
+                     weights_row_stride % 4 == 0 && noise_row_stride % 4 == 0;
+    if (vec) {
+        hipLaunchKernelGGL((race_chunk_kernel<false, true>), dim3(n_rows, a.n_chunks), dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((race_chunk_kernel<false, false>), dim3(n_rows, a.n_chunks), dim3(256), 0, s, a);
+    }
     int st = nvs::check_launch("race chunk kernel");
     if (st != NVS_OK) return st;
     hipLaunchKernelGGL(race_merge_kernel, dim3(n_rows), dim3(64), 0, s, a);
@@ -2680,7 +2744,12 @@ extern "C" int nvs_accept_random(const float* p, const float* q, const int64_t* 
     a.n_accept = n_accept;
     a.out = tail;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(race_chunk_kernel<true>, dim3(batch, a.n_chunks), dim3(256), 0, s, a);
+    const bool vec = vocab % 4 == 0 && nvs::aligned16(p) && nvs::aligned16(q) && nvs::aligned16(noise);
+    if (vec) {
+        hipLaunchKernelGGL((race_chunk_kernel<true, true>), dim3(batch, a.n_chunks), dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((race_chunk_kernel<true, false>), dim3(batch, a.n_chunks), dim3(256), 0, s, a);
+    }
     st = nvs::check_launch("accept_random chunk kernel");
     if (st != NVS_OK) return st;
     hipLaunchKernelGGL(race_merge_kernel, dim3(batch), dim3(64), 0, s, a);

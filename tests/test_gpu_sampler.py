@@ -276,11 +276,12 @@ def test_fused_accept_repeats_and_replays_in_a_graph(device):
         assert torch.equal(n.cpu(), n_want)
 
 
+@pytest.mark.parametrize("vocab", [50000, 50001])   # 16-byte pieces / element loads
 @pytest.mark.parametrize("varlen", [False, True])
-def test_dense_accept_random_is_bit_exact(device, varlen):
-    log_case(f"accept_random dense varlen={varlen}")
+def test_dense_accept_random_is_bit_exact(device, varlen, vocab):
+    log_case(f"accept_random dense varlen={varlen} V={vocab}")
     lens = [1, 8, 3, 5, 2, 7, 4, 6] if varlen else None
-    case = wl.sampler_case(8, 7, 50000, verified_lens=lens, draft_probs_fn=draft_probs)
+    case = wl.sampler_case(8, 7, vocab, verified_lens=lens, draft_probs_fn=draft_probs)
     p = ref.probs_from_logits(case.logits, case.temperatures.repeat_interleave(case.verified_lens)
                               if varlen else case.temperatures.repeat_interleave(8),
                               case.top_k.repeat_interleave(case.verified_lens) if varlen
