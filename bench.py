@@ -180,6 +180,15 @@ def sampler_bench(args, dev):
         ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st_p, None, g.uniforms, g.noise, workspace=ws)
 
     msp = time_gpu(step_p, max(10, args.steps // 2), max(3, args.warmup // 2))
+    # the reference's default sampling (SamplingParams: temperature 1, top_k 0, top_p 1): no truncation, so p is
+    # the softmax over the whole vocabulary and each row's race runs over all of it (p, q and noise rows)
+    st_d = ns.SamplingTensors(g.temperatures, torch.zeros_like(g.top_k), g.top_p, 0, False, False)
+
+    def step_d():
+        ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st_d, None, g.uniforms, g.noise, workspace=ws)
+
+    msd = time_gpu(step_d, max(10, args.steps // 2), max(3, args.warmup // 2))
+    alg_d = alg + 3 * 64 * V * 4
     # the same accept with q as DSpark candidate rows (top-64 + 64 = 128 entries per draft row) instead of dense
     from nvs_amd.layers.markov import CandidateRows
     top = g.q.topk(128, dim=-1)
@@ -193,13 +202,18 @@ def sampler_bench(args, dev):
                                                                         g.noise, workspace=ws), (n, tail))]
     log(f"[bench] fused sampler on bf16 logits: {ms16 * 1e3:.1f} us; top-p 0.9 + temperature 0.7: "
         f"{msp * 1e3:.1f} us; greedy accept (fp32): {msg * 1e3:.1f} us; q as candidate rows: {msc * 1e3:.1f} us "
-        f"(same decisions: {all(same)})")
+        f"(same decisions: {all(same)}); no top-k (the reference's default): {msd * 1e3:.1f} us, "
+        f"{100 * alg_d / (msd * 1e-3) / 1e9 / HBM_PEAK_GBS:.1f}% of 8 TB/s")
     variants = {
         "topp0.9_temp0.7": {"us": round(msp * 1e3, 2), "GBs": round(alg / (msp * 1e-3) / 1e9, 1)},
         "bf16_logits": {"us": round(ms16 * 1e3, 2), "GBs": round(alg / 2 / (ms16 * 1e-3) / 1e9, 1),
                         "algorithmic_bytes": alg // 2},
         "candidate_rows_q": {"us": round(msc * 1e3, 2), "GBs": round(alg / (msc * 1e-3) / 1e9, 1),
                              "candidates": 128, "same_decisions_as_dense_q": all(same)},
+        "no_topk_default_sampling": {"us": round(msd * 1e3, 2), "GBs": round(alg_d / (msd * 1e-3) / 1e9, 1),
+                                     "algorithmic_bytes": alg_d,
+                                     "bytes_are": "every logit once, plus each row's race over its p, q and noise "
+                                                  "rows"},
         "greedy_fp32": {"us": round(msg * 1e3, 2), "GBs": round(alg / (msg * 1e-3) / 1e9, 1),
                         "algorithmic_bytes": alg, "kernel": "argmax_kernel + greedy_finalize_kernel"},
     }

@@ -55,6 +55,15 @@ struct PosRecord {
 };
 static_assert(sizeof(PosRecord) == 32, "record layout");
 
+// The race of a batch row whose tail position does not truncate, handed by the accept kernel's row finish to
+// dense_race_chunk_kernel / dense_race_merge_kernel (used when no row truncates, so the host launches them).
+struct DenseRace {
+    int64_t pos;     // logit row of the position after the accepted prefix
+    int64_t qrow;    // q row b * k + min(n, k - 1); -1 for the bonus position (w = p)
+    float m, z, temp;
+    int valid;       // 1: this row's tail comes from the dense race
+};
+
 // Records cross workgroups (and XCDs) through device-scope atomic stores and loads, which the gfx950 backend
 // performs at the device's coherence point (sc1) rather than in an XCD's own L2. That keeps them out of the L2
 // write-back a release fence would force on every position.
@@ -101,6 +110,9 @@ struct SelArgs {
     int k;
     PosRecord* rec;
     int* counters;        // [batch] finished positions per row; zero between calls
+    DenseRace* dense_race;   // non-null: rows without truncation leave their race to the dense race kernels
+    uint64_t* dense_partial; // [batch, dense_chunks] best keys of the dense race's chunks
+    int dense_chunks;
     int64_t* n_accept;
     int64_t* tail;
     // dense outputs
@@ -719,6 +731,19 @@ __device__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L
                     a.n_accept[b] = n;
                     a.tail[b] = r.race;
                     a.counters[b] = 0;   // ready for the next call
+                    if (a.dense_race != nullptr) a.dense_race[b].valid = 0;
+                } else if (a.dense_race != nullptr) {
+                    // the race over the whole vocabulary runs in the dense race kernels, spread over the chip
+                    DenseRace d;
+                    d.pos = min(start + n, a.n_pos - 1);
+                    d.qrow = (n == L - 1) ? -1 : b * kd + (n < kd - 1 ? n : kd - 1);
+                    d.m = r.m;
+                    d.z = r.z;
+                    d.temp = r.temp;
+                    d.valid = 1;
+                    a.dense_race[b] = d;
+                    a.n_accept[b] = n;
+                    a.counters[b] = 0;
                 }
             }
             break;
@@ -727,7 +752,7 @@ __device__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L
     __syncthreads();
     const int64_t n = sh.fin_n;
     const PosRecord r = sh.fin_rec;
-    if (r.flags & kFlagDense) {
+    if ((r.flags & kFlagDense) && a.dense_race == nullptr) {
         const int64_t pos = min(start + n, a.n_pos - 1);
         const bool bonus = (n == L - 1);
         const int64_t qn = n < kd - 1 ? n : kd - 1;
@@ -1532,22 +1557,55 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
     bool record_done = false;   // the wave-0 epilogue already wrote this position's record
     int kept_source = kKeptInRow;   // where a Markov draw finds the kept values
     if (!truncating) {
-        load_decision();
-        // online max / sum-exp over the whole row
+        // online max / sum-exp over the whole row, one batch at a time: the batch's max rescales the running sum
+        // once, then every value adds exp(s - m). NaN (and the padding past the row) adds nothing; -inf adds 0.
         float m = -INFINITY, z = 0.f;
-        for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
-            float v[kVpt];
-            load_vals<DT, VEC>(row, e0, a.vocab, v);
+        auto accum = [&](float (&v)[kVpt], int bi) {
+            const int64_t e0 = static_cast<int64_t>(bi) * kBatch;
+            const bool tail_batch = e0 + kBatch > a.vocab;
+            float bm = -INFINITY;
 #pragma unroll
             for (int vi = 0; vi < kVpt; ++vi) {
-                const float s = scale_logit(v[vi], temp, unit_temp);
-                if (s != s) continue;
-                if (s > m) {
-                    z = z * expf(m - s) + 1.f;
-                    m = s;
-                } else {
-                    z += expf(s - m);
-                }
+                float s = scale_logit(v[vi], temp, unit_temp);
+                if (tail_batch && val_index<DT>(e0, vi) >= a.vocab) s = NAN;
+                v[vi] = s;
+                bm = fmaxf(bm, s);
+            }
+            if (bm > m) {
+                z = z * expf(m - bm);
+                m = bm;
+            }
+            if (m == -INFINITY) return;
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) z += (v[vi] == v[vi]) ? expf(v[vi] - m) : 0.f;
+        };
+        const int nb = static_cast<int>((a.vocab + kBatch - 1) / kBatch);
+        // the same load pipeline as the truncating pass: three buffers in a ring (two with element loads)
+        float ra[kVpt], rb[kVpt], rc[kVpt];
+        load_vals<DT, VEC, false>(row, 0, a.vocab, ra);
+        load_vals<DT, VEC, false>(row, kBatch, a.vocab, rb);
+        if constexpr (VEC) load_vals<DT, VEC, false>(row, 2 * kBatch, a.vocab, rc);
+        load_decision();
+        if constexpr (VEC) {
+            for (int bi = 0;;) {
+                accum(ra, bi);
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 3) * kBatch, a.vocab, ra);
+                if (++bi >= nb) break;
+                accum(rb, bi);
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 3) * kBatch, a.vocab, rb);
+                if (++bi >= nb) break;
+                accum(rc, bi);
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 3) * kBatch, a.vocab, rc);
+                if (++bi >= nb) break;
+            }
+        } else {
+            for (int bi = 0;;) {
+                accum(ra, bi);
+                if (++bi >= nb) break;
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 1) * kBatch, a.vocab, ra);
+                accum(rb, bi);
+                if (++bi >= nb) break;
+                load_vals<DT, VEC, false>(row, static_cast<int64_t>(bi + 1) * kBatch, a.vocab, rb);
             }
         }
         const uint32_t mk = block_max_u32(m == -INFINITY ? 0u : nvs::float_key(m), sh);
@@ -2797,15 +2855,128 @@ extern "C" int nvs_accept_greedy(const void* logits, int logits_dtype, int64_t l
 }
 
 // Workspace of the fused accept: one 32-byte record per position (the per-row counters are a separate argument).
+// ---------------------------------------------------------------- dense race of the fused accept
+// Rows that do not truncate: the tail is argmax_i w_i / E_i over the whole vocabulary with p_i = exp(s_i - m) / Z
+// recomputed from the tail position's logits (s = logit / temperature, NaN gives p = 0) and w = p for the bonus
+// position, max(p - q, 0) otherwise: the same scores as the row finish's own loop, spread over (row, chunk)
+// workgroups like the dense race kernels, then merged per row.
+
+// Four consecutive logits of a row as floats: one 16-byte load (fp32) or one 8-byte load (16-bit).
+template <int DT>
+__device__ __forceinline__ float4 load4_as_float(const char* row, int64_t j) {
+    if constexpr (DT == NVS_DTYPE_F32) {
+        return reinterpret_cast<const float4*>(row)[j];
+    } else {
+        const uint2 w = reinterpret_cast<const uint2*>(row)[j];
+        auto cv = [](uint32_t h) {
+            if constexpr (DT == NVS_DTYPE_BF16) return nvs::bf16_bits_to_float(static_cast<uint16_t>(h));
+            else return nvs::f16_bits_to_float(static_cast<uint16_t>(h));
+        };
+        return make_float4(cv(w.x & 0xffffu), cv(w.x >> 16), cv(w.y & 0xffffu), cv(w.y >> 16));
+    }
+}
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void dense_race_chunk_kernel(SelArgs a) {
+    __shared__ uint64_t red[4];
+    const int64_t r = blockIdx.x;
+    const int c = blockIdx.y;
+    const DenseRace d = a.dense_race[r];
+    uint64_t best = 0;
+    if (d.valid) {
+        const int64_t i0 = static_cast<int64_t>(c) * kRaceChunk;
+        const int64_t i1 = min(i0 + kRaceChunk, a.vocab);
+        const float* erow = a.noise + r * a.vocab;
+        const char* row = static_cast<const char*>(a.logits) + d.pos * a.row_stride * nvs::dtype_size(DT);
+        const bool bonus = d.qrow < 0;
+        const float* qrow = a.q + (bonus ? 0 : d.qrow) * a.vocab;
+        const float mu = (d.m == -INFINITY) ? 0.f : d.m;
+        const bool unit_temp = (d.temp == 1.f);
+        auto key_of = [&](float x, float q, float e, int64_t i) {
+            const float sc = scale_logit(x, d.temp, unit_temp);
+            const float p = (sc == sc) ? expf(sc - mu) / d.z : 0.f;
+            const float w = bonus ? p : fmaxf(p - q, 0.f);
+            const float score = w / e;
+            return (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+                   static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
+        };
+        if constexpr (VEC) {
+            // every load first (noise, logits, q), from pieces clamped into the chunk
+            float4 ev[kRacePer], xv[kRacePer], qv[kRacePer];
+#pragma unroll
+            for (int m = 0; m < kRacePer; ++m) {
+                const int64_t j = min((i0 >> 2) + threadIdx.x + 256 * m, (i1 >> 2) - 1);
+                ev[m] = reinterpret_cast<const float4*>(erow)[j];
+                xv[m] = load4_as_float<DT>(row, j);
+                qv[m] = reinterpret_cast<const float4*>(qrow)[j];
+            }
+#pragma unroll
+            for (int m = 0; m < kRacePer; ++m) {
+                const int64_t j = (i0 >> 2) + threadIdx.x + 256 * m;
+                if (j >= (i1 >> 2)) continue;
+                const float x4[4] = {xv[m].x, xv[m].y, xv[m].z, xv[m].w};
+                const float q4[4] = {qv[m].x, qv[m].y, qv[m].z, qv[m].w};
+                const float e4[4] = {ev[m].x, ev[m].y, ev[m].z, ev[m].w};
+#pragma unroll
+                for (int l = 0; l < 4; ++l) {
+                    const uint64_t k64 = key_of(x4[l], q4[l], e4[l], 4 * j + l);
+                    best = best > k64 ? best : k64;
+                }
+            }
+        } else {
+            for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+                const uint64_t k64 = key_of(nvs::load_as_float<DT>(row, i), bonus ? 0.f : qrow[i], erow[i], i);
+                best = best > k64 ? best : k64;
+            }
+        }
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t all = 0;
+        for (int w = 0; w < 4; ++w) all = red[w] > all ? red[w] : all;
+        a.dense_partial[r * a.dense_chunks + c] = all;
+    }
+}
+
+__global__ __launch_bounds__(64) void dense_race_merge_kernel(SelArgs a) {
+    const int64_t r = blockIdx.x;
+    if (!a.dense_race[r].valid) return;   // the row's tail is its position's own race, already written
+    uint64_t best = 0;
+    for (int c = threadIdx.x; c < a.dense_chunks; c += 64) {
+        const uint64_t v = a.dense_partial[r * a.dense_chunks + c];
+        best = best > v ? best : v;
+    }
+    best = wave_max_u64(best);
+    if (threadIdx.x == 0) a.tail[r] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
+}
+
+// Workspace of the fused accept: the position records, then (no truncating row) the dense races and their chunks.
+struct AcceptLayout {
+    size_t dense_off, partial_off, bytes;
+};
+AcceptLayout accept_layout(int64_t batch, int64_t n_pos, int64_t vocab, bool dense) {
+    AcceptLayout l;
+    l.bytes = static_cast<size_t>(n_pos) * sizeof(PosRecord);
+    l.dense_off = l.partial_off = 0;
+    if (dense) {
+        l.dense_off = nvs::align_up(l.bytes, 256);
+        l.partial_off = nvs::align_up(l.dense_off + static_cast<size_t>(batch) * sizeof(DenseRace), 256);
+        l.bytes = l.partial_off + static_cast<size_t>(batch) * static_cast<size_t>(race_chunks(vocab)) * 8;
+    }
+    return l;
+}
+
 extern "C" int nvs_spec_accept_workspace_size(int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
                                               int max_top_k, size_t* bytes) {
     nvs::clear_error();
     (void)num_drafts;
-    (void)vocab;
-    NVS_CHECK(bytes != nullptr && n_pos >= 0 && batch >= 0, NVS_ERR_INVALID, "spec_accept_workspace_size: bad args");
+    NVS_CHECK(bytes != nullptr && n_pos >= 0 && batch >= 0 && vocab > 0, NVS_ERR_INVALID,
+              "spec_accept_workspace_size: bad args");
     const int st = check_topk(max_top_k);
     if (st != NVS_OK) return st;
-    *bytes = static_cast<size_t>(n_pos) * sizeof(PosRecord);
+    *bytes = accept_layout(batch, n_pos, vocab, max_top_k == 0).bytes;
     return NVS_OK;
 }
 
@@ -2830,9 +3001,12 @@ static int spec_accept_impl(const void* logits, int logits_dtype, int64_t logits
     NVS_CHECK(verified_lens != nullptr || n_pos == batch * (num_drafts + 1), NVS_ERR_INVALID,
               "spec_accept: logits have %lld positions, expected batch*(k+1) = %lld", (long long)n_pos,
               (long long)(batch * (num_drafts + 1)));
-    const size_t need = static_cast<size_t>(n_pos) * sizeof(PosRecord);
-    NVS_CHECK(workspace != nullptr && workspace_bytes >= need, NVS_ERR_WORKSPACE,
-              "spec_accept: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    // No row truncates (the reference's default sampling): each row's race over the whole vocabulary runs in
+    // the dense race kernels after the accept kernel, spread over (row, chunk) workgroups.
+    const bool dense = max_top_k == 0;
+    const AcceptLayout lay = accept_layout(batch, n_pos, vocab, dense);
+    NVS_CHECK(workspace != nullptr && workspace_bytes >= lay.bytes, NVS_ERR_WORKSPACE,
+              "spec_accept: workspace of %zu bytes needed, %zu given", lay.bytes, workspace_bytes);
     SelArgs a{};
     a.logits = logits;
     a.row_stride = logits_row_stride;
@@ -2859,7 +3033,32 @@ static int spec_accept_impl(const void* logits, int logits_dtype, int64_t logits
     a.counters = row_counters;
     a.n_accept = n_accept;
     a.tail = tail;
-    return launch_select<kModeAccept>(logits_dtype, a, static_cast<hipStream_t>(stream));
+    if (dense) {
+        a.dense_race = reinterpret_cast<DenseRace*>(static_cast<char*>(workspace) + lay.dense_off);
+        a.dense_partial = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + lay.partial_off);
+        a.dense_chunks = static_cast<int>(race_chunks(vocab));
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    st = launch_select<kModeAccept>(logits_dtype, a, s);
+    if (st != NVS_OK || !dense) return st;
+    const int es = nvs::dtype_size(logits_dtype);
+    const bool vec = vocab % 4 == 0 && logits_row_stride % 4 == 0 && nvs::aligned16(noise) && nvs::aligned16(q) &&
+                     (reinterpret_cast<uintptr_t>(logits) % (4 * es)) == 0;
+    const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>(a.dense_chunks));
+    if (logits_dtype == NVS_DTYPE_F32) {
+        if (vec) hipLaunchKernelGGL((dense_race_chunk_kernel<NVS_DTYPE_F32, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((dense_race_chunk_kernel<NVS_DTYPE_F32, false>), grid, dim3(256), 0, s, a);
+    } else if (logits_dtype == NVS_DTYPE_BF16) {
+        if (vec) hipLaunchKernelGGL((dense_race_chunk_kernel<NVS_DTYPE_BF16, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((dense_race_chunk_kernel<NVS_DTYPE_BF16, false>), grid, dim3(256), 0, s, a);
+    } else {
+        if (vec) hipLaunchKernelGGL((dense_race_chunk_kernel<NVS_DTYPE_F16, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((dense_race_chunk_kernel<NVS_DTYPE_F16, false>), grid, dim3(256), 0, s, a);
+    }
+    st = nvs::check_launch("spec_accept dense race");
+    if (st != NVS_OK) return st;
+    hipLaunchKernelGGL(dense_race_merge_kernel, dim3(static_cast<unsigned>(batch)), dim3(64), 0, s, a);
+    return nvs::check_launch("spec_accept dense race merge");
 }
 
 extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_stride,

@@ -177,6 +177,11 @@ def draft_probs(draft_logits, temps, tk, tp):
     ("topp_temps", dict(batch=8, num_drafts=3, vocab=32000, top_k=[64, 20, 5, 64] * 2,
                         top_p=[0.9, 1.0, 0.6, 0.95] * 2, temperature=[0.7, 1.0, 1.5, 1.0] * 2)),
     ("dense_rows", dict(batch=4, num_drafts=3, vocab=32000, top_k=[0, 64, 0, 10])),
+    # no row truncates (the reference's default sampling): the races run in the dense race kernels
+    ("no_topk", dict(batch=16, num_drafts=7, vocab=151936, top_k=0)),
+    ("no_topk_bf16_varlen_temps", dict(batch=8, num_drafts=7, vocab=151936, top_k=0, logits_dtype=torch.bfloat16,
+                                       verified_lens=[1, 8, 3, 5, 2, 7, 4, 6], temperature=[0.7, 1.0, 1.3, 1.0] * 2)),
+    ("no_topk_odd_vocab", dict(batch=4, num_drafts=3, vocab=32001, top_k=0, temperature=[0.7, 1.0] * 2)),
     ("bf16_logits", dict(batch=8, num_drafts=7, vocab=151936, logits_dtype=torch.bfloat16)),
     ("small_sigma", dict(batch=8, num_drafts=7, vocab=151936, sigma=0.5)),
 ])
@@ -245,14 +250,16 @@ def test_probs_on_ordered_logits(device, kind):
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-7)
 
 
-def test_fused_accept_repeats_and_replays_in_a_graph(device):
+@pytest.mark.parametrize("top_k", [64, 0])   # 0: the dense race kernels run in the graph too
+def test_fused_accept_repeats_and_replays_in_a_graph(device, top_k):
     """The per-row counters the fused accept keeps in its workspace return to zero after every call: repeated eager
     calls and HIP-graph replays give the same (bit-exact) answer."""
-    log_case("fused accept repeated calls and graph replays")
-    case = wl.sampler_case(16, 7, 32000, verified_lens=[1, 8, 3, 5, 2, 7, 4, 6] * 2, draft_probs_fn=draft_probs)
+    log_case(f"fused accept repeated calls and graph replays top_k={top_k}")
+    case = wl.sampler_case(16, 7, 32000, top_k=top_k, verified_lens=[1, 8, 3, 5, 2, 7, 4, 6] * 2,
+                           draft_probs_fn=draft_probs)
     n_want, tail_want = run_oracle(case)
     g = case.to(device)
-    st = ns.SamplingTensors(g.temperatures, g.top_k, g.top_p, case.max_top_k, case.has_top_p, True)
+    st = ns.SamplingTensors(g.temperatures, g.top_k, g.top_p, case.max_top_k, case.has_top_p, top_k > 0)
 
     def call():
         return ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st, g.verified_lens, g.uniforms, g.noise)
