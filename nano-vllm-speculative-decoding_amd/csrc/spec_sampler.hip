@@ -1559,18 +1559,23 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
     if (!truncating) {
         // online max / sum-exp over the whole row, one batch at a time: the batch's max rescales the running sum
         // once, then every value adds exp(s - m). NaN (and the padding past the row) adds nothing; -inf adds 0.
+        // The pass is bound by its arithmetic: the division by the temperature and the mask of the last, partial
+        // batch sit behind uniform branches (as selects they would be computed for every value).
         float m = -INFINITY, z = 0.f;
+        const int nb = static_cast<int>((a.vocab + kBatch - 1) / kBatch);
         auto accum = [&](float (&v)[kVpt], int bi) {
-            const int64_t e0 = static_cast<int64_t>(bi) * kBatch;
-            const bool tail_batch = e0 + kBatch > a.vocab;
-            float bm = -INFINITY;
+            if (bi == nb - 1) {
+                const int64_t e0 = static_cast<int64_t>(bi) * kBatch;
 #pragma unroll
-            for (int vi = 0; vi < kVpt; ++vi) {
-                float s = scale_logit(v[vi], temp, unit_temp);
-                if (tail_batch && val_index<DT>(e0, vi) >= a.vocab) s = NAN;
-                v[vi] = s;
-                bm = fmaxf(bm, s);
+                for (int vi = 0; vi < kVpt; ++vi) v[vi] = val_index<DT>(e0, vi) < a.vocab ? v[vi] : NAN;
             }
+            if (!unit_temp) {
+#pragma unroll
+                for (int vi = 0; vi < kVpt; ++vi) v[vi] = v[vi] / temp;
+            }
+            float bm = v[0];
+#pragma unroll
+            for (int vi = 1; vi < kVpt; ++vi) bm = fmaxf(bm, v[vi]);
             if (bm > m) {
                 z = z * expf(m - bm);
                 m = bm;
@@ -1579,7 +1584,6 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
 #pragma unroll
             for (int vi = 0; vi < kVpt; ++vi) z += (v[vi] == v[vi]) ? expf(v[vi] - m) : 0.f;
         };
-        const int nb = static_cast<int>((a.vocab + kBatch - 1) / kBatch);
         // the same load pipeline as the truncating pass: three buffers in a ring (two with element loads)
         float ra[kVpt], rb[kVpt], rc[kVpt];
         load_vals<DT, VEC, false>(row, 0, a.vocab, ra);
@@ -2892,8 +2896,8 @@ __global__ __launch_bounds__(256) void dense_race_chunk_kernel(SelArgs a) {
         const float* qrow = a.q + (bonus ? 0 : d.qrow) * a.vocab;
         const float mu = (d.m == -INFINITY) ? 0.f : d.m;
         const bool unit_temp = (d.temp == 1.f);
-        auto key_of = [&](float x, float q, float e, int64_t i) {
-            const float sc = scale_logit(x, d.temp, unit_temp);
+        // sc: the logit already divided by the temperature (behind a uniform branch, not a select)
+        auto key_of = [&](float sc, float q, float e, int64_t i) {
             const float p = (sc == sc) ? expf(sc - mu) / d.z : 0.f;
             const float w = bonus ? p : fmaxf(p - q, 0.f);
             const float score = w / e;
@@ -2910,6 +2914,15 @@ __global__ __launch_bounds__(256) void dense_race_chunk_kernel(SelArgs a) {
                 xv[m] = load4_as_float<DT>(row, j);
                 qv[m] = reinterpret_cast<const float4*>(qrow)[j];
             }
+            if (!unit_temp) {
+#pragma unroll
+                for (int m = 0; m < kRacePer; ++m) {
+                    xv[m].x = xv[m].x / d.temp;
+                    xv[m].y = xv[m].y / d.temp;
+                    xv[m].z = xv[m].z / d.temp;
+                    xv[m].w = xv[m].w / d.temp;
+                }
+            }
 #pragma unroll
             for (int m = 0; m < kRacePer; ++m) {
                 const int64_t j = (i0 >> 2) + threadIdx.x + 256 * m;
@@ -2925,7 +2938,8 @@ __global__ __launch_bounds__(256) void dense_race_chunk_kernel(SelArgs a) {
             }
         } else {
             for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
-                const uint64_t k64 = key_of(nvs::load_as_float<DT>(row, i), bonus ? 0.f : qrow[i], erow[i], i);
+                const uint64_t k64 = key_of(scale_logit(nvs::load_as_float<DT>(row, i), d.temp, unit_temp),
+                                            bonus ? 0.f : qrow[i], erow[i], i);
                 best = best > k64 ? best : k64;
             }
         }
