@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NVS_ABI_VERSION 6
+#define NVS_ABI_VERSION 7
 
 typedef enum {
     NVS_OK = 0,
@@ -122,7 +122,11 @@ int nvs_qk_norm_rope_store(const void* q, int64_t q_token_stride, const void* k,
  * capture passes max_model_len); the grid depends only on the host integers, so a captured launch stays valid for
  * any device lengths within those bounds.
  * workspace: device memory of at least nvs_paged_attention_workspace_size(...) bytes (may be NULL when that is 0);
- * no initialisation needed.
+ * no initialisation needed. One launch: when the plan splits a row's keys, each split writes an fp32 partial to
+ * the workspace and the (row, kv head, query tile) unit's last split to finish merges them. unit_counters: int32
+ * [n_rows * n_kv_heads * ceil((n_heads/n_kv_heads) * max_seqlen_q / 32)] device buffer that is zero on entry;
+ * every call leaves it zero again (keep one zero-filled buffer and reuse it; calls sharing it must be ordered on
+ * one stream). It may be NULL when the workspace size is 0 (no split).
  * Bounds: n_tokens (rows of q / out), cache_blocks (blocks of each cache) and bt_width (valid entries per block
  * table row) bound every index the kernel derives from device metadata; inconsistent metadata gives wrong
  * numbers for the rows concerned, never an access outside the buffers. */
@@ -139,7 +143,7 @@ int nvs_paged_attention(const void* q, int64_t q_token_stride, int64_t q_head_st
                         int n_heads, int n_kv_heads, int head_dim, int block_size,
                         float scale, int causal, int dtype,
                         void* out, int64_t out_token_stride, int64_t out_head_stride,
-                        void* workspace, size_t workspace_bytes, void* stream);
+                        int32_t* unit_counters, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------------------------ sampler
  * Shared conventions (nanovllm/layers/spec_sampler.py):
@@ -167,21 +171,28 @@ int nvs_truncate_logits(const float* scaled, int64_t scaled_row_stride, int64_t 
                         float* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* race / sample (spec_sampler.py:99-111): out[r] = argmax_i weights[r,i] / noise[r,i] (first index wins ties),
- * weights and noise fp32 [n_rows, V] with the given row strides. */
+ * weights and noise fp32 [n_rows, V] with the given row strides.
+ * One launch over (row, vocabulary chunk) workgroups: the last chunk of each row to finish picks the row's winner.
+ * row_counters: int32 [n_rows] device buffer that is zero on entry; every call leaves it zero again (keep one
+ * zero-filled buffer and reuse it; calls sharing it must be ordered on one stream). workspace: scratch of
+ * nvs_race_workspace_size bytes, no initialisation needed. */
 int nvs_race(const float* weights, int64_t weights_row_stride, const float* noise, int64_t noise_row_stride,
-             int64_t n_rows, int64_t vocab, int64_t* out, void* workspace, size_t workspace_bytes, void* stream);
+             int64_t n_rows, int64_t vocab, int64_t* out, int32_t* row_counters, void* workspace,
+             size_t workspace_bytes, void* stream);
 int nvs_race_workspace_size(int64_t n_rows, int64_t vocab, size_t* bytes);
 
 /* accept_random_varlen (spec_sampler.py:123-150) over dense probabilities, with the generator's draws passed in:
  * uniforms = torch.rand(B, k) and noise = exponential_noise_([B, V]) drawn in that order by the caller.
  * p [T, V] fp32 (row stride V), q [B, k, V] fp32 contiguous, drafts [B, k] int64, verified_lens [B] int64 in
  * 1..k+1 summing to T (NULL = every row verifies k+1 = accept_random, spec_sampler.py:114-120).
- * Outputs n_accept [B] int64 and tail [B] int64. */
+ * Outputs n_accept [B] int64 and tail [B] int64. One launch, like nvs_race; row_counters: int32 [B], zero on
+ * entry and left zero, as for nvs_race. */
 int nvs_accept_random_workspace_size(int64_t batch, int64_t vocab, size_t* bytes);
 int nvs_accept_random(const float* p, const float* q, const int64_t* drafts, const int64_t* verified_lens,
                       const float* uniforms, const float* noise,
                       int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
-                      int64_t* n_accept, int64_t* tail, void* workspace, size_t workspace_bytes, void* stream);
+                      int64_t* n_accept, int64_t* tail, int32_t* row_counters, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 /* accept_greedy_varlen (spec_sampler.py:153-169): target tokens = argmax of each logit row (first max wins);
  * a draft is accepted iff it equals the target token at its position; tail = the target token after the

@@ -40,15 +40,15 @@ SIGNATURES = {
                                _i64, _i64, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32, _p],
     "nvs_paged_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _size_p],
     "nvs_paged_attention": [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i32, _p, _p, _p, _i32,
-                            _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _i64, _i64, _p,
+                            _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _i64, _i64, _p, _p,
                             ctypes.c_size_t, _p],
     "nvs_probs_from_logits_workspace_size": [_i64, _i64, _i32, _size_p],
     "nvs_probs_from_logits": [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _i32, _i32, _p, _p, ctypes.c_size_t, _p],
     "nvs_truncate_logits": [_p, _i64, _i64, _i64, _i64, _p, _p, _i32, _i32, _p, _p, ctypes.c_size_t, _p],
-    "nvs_race": [_p, _i64, _p, _i64, _i64, _i64, _p, _p, ctypes.c_size_t, _p],
+    "nvs_race": [_p, _i64, _p, _i64, _i64, _i64, _p, _p, _p, ctypes.c_size_t, _p],
     "nvs_race_workspace_size": [_i64, _i64, _size_p],
     "nvs_accept_random_workspace_size": [_i64, _i64, _size_p],
-    "nvs_accept_random": [_p, _p, _p, _p, _p, _p, _i64, _i32, _i64, _i64, _p, _p, _p, ctypes.c_size_t, _p],
+    "nvs_accept_random": [_p, _p, _p, _p, _p, _p, _i64, _i32, _i64, _i64, _p, _p, _p, _p, ctypes.c_size_t, _p],
     "nvs_accept_greedy_workspace_size": [_i64, _i64, _size_p],
     "nvs_accept_greedy": [_p, _i32, _i64, _p, _p, _i64, _i32, _i64, _i64, _p, _p, _p, ctypes.c_size_t, _p],
     "nvs_spec_accept_workspace_size": [_i64, _i32, _i64, _i64, _i32, _size_p],
@@ -145,8 +145,9 @@ _persistent: dict = {}
 
 def persistent_workspace(name: str, nbytes: int, device: torch.device) -> torch.Tensor:
     """A zero-initialised device buffer kept across calls, for kernels that keep counters in it and leave them at
-    zero when they finish (the fused accept's row counters). One buffer per (name, device); calls that share it
-    must be ordered on one stream. It is created outside graph capture: warm up once eagerly before capturing."""
+    zero when they finish (the row and unit counters of the one-launch accept, race and split-key attention). One
+    buffer per (name, device); calls that share it must be ordered on one stream. It is created outside graph
+    capture: warm up once eagerly before capturing."""
     key = (name, device.type, device.index)
     buf = _persistent.get(key)
     if buf is None or buf.numel() < nbytes:

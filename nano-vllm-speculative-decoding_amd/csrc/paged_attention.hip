@@ -14,7 +14,9 @@
 //   a captured graph serves every batch); each wave of the workgroup takes every 4th
 //   32-key chunk of its split and keeps its own online-softmax state. The 4 waves are merged in LDS
 //   (deterministic order); a row with a single split writes bf16 output directly, otherwise each split writes an
-//   fp32 partial (O, max, sum) and attn_combine_kernel merges them with the log-sum-exp rule.
+//   fp32 partial (O, max, sum) at the device's coherence point and counts itself on the unit's counter; the
+//   unit's last split to finish merges every partial with the log-sum-exp rule, in split order (so the result
+//   does not depend on which split finished last), and writes the bf16 output. One launch either way.
 //
 // Per chunk of 32 keys, per wave (lane l: packed row nl = l % 32, half gi = l / 32):
 //   load    K and V rows of the chunk with coalesced streaming 16-byte loads (4 keys x 256 B per instruction,
@@ -30,7 +32,6 @@
 #include "nvs_common.hpp"
 
 #include <cmath>
-#include <cstdlib>
 
 namespace {
 
@@ -52,6 +53,10 @@ constexpr int kRowStride = kHeadDim + 8;                 // bf16 elements per st
 constexpr int kTileElems = kChunk * kRowStride;          // one 32-key tile
 constexpr int kWaveElems = 2 * kTileElems;               // K tile + V tile
 constexpr int kObStride = 33;                            // fp32 per dim row of the cross-wave reduction buffer
+// A split's partial is staged in LDS past the reduction buffer: [32 rows][128 dims] fp32 (16-byte pieces swizzled
+// by row), then the rows' (max, sum) pairs.
+constexpr int kStageOffset = kHeadDim * kObStride;       // in floats
+constexpr int kMaxSplits = 64;                           // the merge keeps [splits][32] (max, sum) pairs in LDS
 // Query tile in LDS: [32 packed rows][128 dims] bf16 with the same padded rows (B-operand reads of 32 rows at one
 // column per half-wave).
 constexpr int kQsStride = kRowStride;
@@ -77,6 +82,7 @@ struct AttnArgs {
     int64_t o_ts, o_hs;
     float* part_o;   // [units, n_splits, 32, 128]
     float* part_ml;  // [units, n_splits, 32, 2]
+    int* counters;   // [units] splits of the unit finished; zero between calls
     int n_splits, split_tokens, q_tiles;   // split_tokens: the smallest split of a row with several
 };
 
@@ -98,13 +104,15 @@ __device__ __forceinline__ RowInfo row_info(const AttnArgs& a, int r) {
     return ri;
 }
 
-// Keys per split of a row with lk keys: the row spread evenly over the grid's n_splits splits, rounded up to whole
-// 32-key chunks (a chunk never straddles a page), at least min_tokens. ceil(lk / that) <= n_splits, so a length
-// above max_seqlen_k cannot send the combine past the partial buffers.
+// Keys per split of a row with lk keys: the row cut into n = clamp(lk / min_tokens, 1, n_splits) equal splits
+// (so each holds at least min_tokens keys when there are several), rounded up to whole 32-key chunks (a chunk
+// never straddles a page). ceil(lk / that) <= n <= n_splits, so a length above max_seqlen_k cannot send the merge
+// past the partial buffers.
 __device__ __forceinline__ int row_split_tokens(int lk, int min_tokens, int n_splits) {
     if (n_splits <= 1) return max(lk, 1);
-    const int even = (lk + n_splits - 1) / n_splits;
-    return max((even + kChunk - 1) / kChunk * kChunk, min_tokens);
+    const int n = max(1, min(n_splits, lk / min_tokens));
+    const int even = (lk + n - 1) / n;
+    return max((even + kChunk - 1) / kChunk * kChunk, kChunk);
 }
 
 // Splits holding keys of a row (at least one, so a row without keys still writes zeros).
@@ -120,10 +128,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
     __shared__ float sm_m[kWaves][kTileRows];
     __shared__ float sm_l[kWaves][kTileRows];
 
-    const int r = blockIdx.z;
-    const int g = blockIdx.y / a.q_tiles;
-    const int qt = blockIdx.y - g * a.q_tiles;
-    const int s = blockIdx.x;
+    // grid (kv head x query tile, row, split): every unit's first split is dispatched before any second split, so
+    // the idle splits of short rows (s >= the row's split count) sit at the end of the dispatch order
+    const int r = blockIdx.y;
+    const int g = blockIdx.x / a.q_tiles;
+    const int qt = blockIdx.x - g * a.q_tiles;
+    const int s = blockIdx.z;
     const RowInfo ri = row_info(a, r);
     const int n_base = qt * kTileRows;
     if (ri.lq <= 0 || n_base >= a.group * ri.lq) return;
@@ -138,6 +148,36 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
     const int lane = tid & 63;
     const int nl = lane & 31;
     const int gi = lane >> 5;
+    const int32_t* btr = a.bt + static_cast<int64_t>(r) * a.bt_rs;
+    // Coalesced loads: lane -> key 4i + lane/16 of the chunk, 16 B piece lane%16 of that key's 256 B head row.
+    const int ld_key = lane >> 4;
+    const int ld_piece = lane & 15;
+    const int64_t head_off = static_cast<int64_t>(g) * a.c_hs + 8 * ld_piece;
+    const int nch = (k1 - k0 + kChunk - 1) / kChunk;
+
+    // K and V of chunk c into registers (clamped into [0, Lk) so a tail chunk never reads outside the row's pages;
+    // a 32-key chunk never straddles a page because block_size is a multiple of 32).
+    auto load_chunk = [&](int c, u32x4 (&kr)[8], u32x4 (&vr)[8]) {
+        const int tb = k0 + c * kChunk;
+        const int page = min(tb / a.block_size, a.bt_width - 1);
+        int64_t blk = btr[page];
+        blk = blk < 0 ? 0 : (blk >= a.n_blocks ? a.n_blocks - 1 : blk);
+        const int64_t base = blk * a.c_bs + head_off;
+        const int in_page = tb - (tb / a.block_size) * a.block_size;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int t = min(tb + 4 * i + ld_key, ri.lk - 1);
+            const int64_t off = base + static_cast<int64_t>(in_page + (t - tb)) * a.c_ts;
+            // streaming (non-temporal) loads: every K/V byte is read exactly once, so keep it out of the caches'
+            // normal replacement; measured ~15% more bandwidth than default loads on MI355X for this stream
+            kr[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.kc + off));
+            vr[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vc + off));
+        }
+    };
+
+    // This wave's first chunk is requested before the query tile, so the two loads are in flight together.
+    u32x4 kr[8], vr[8];
+    if (wave < nch) load_chunk(wave, kr, vr);
 
     // The query tile -> LDS (zeros for packed rows past the row's Lq): 32 rows x 256 B, one 16 B piece per thread
     // and pass.
@@ -168,39 +208,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
     uint16_t* ks = tiles + wave * kWaveElems;   // this wave's K tile
     uint16_t* vs = ks + kTileElems;             // and V tile
     const uint16_t* qrow = qs + nl * kQsStride + 8 * gi;
-    const int32_t* btr = a.bt + static_cast<int64_t>(r) * a.bt_rs;
-    // Coalesced loads: lane -> key 4i + lane/16 of the chunk, 16 B piece lane%16 of that key's 256 B head row.
-    const int ld_key = lane >> 4;
-    const int ld_piece = lane & 15;
-    const int64_t head_off = static_cast<int64_t>(g) * a.c_hs + 8 * ld_piece;
 
     float m_run = -INFINITY;
     float l_run = 0.f;
     f32x16 o[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] = f32x16{};
-
-    const int nch = (k1 - k0 + kChunk - 1) / kChunk;
-
-    // K and V of chunk c into registers (clamped into [0, Lk) so a tail chunk never reads outside the row's pages;
-    // a 32-key chunk never straddles a page because block_size is a multiple of 32).
-    auto load_chunk = [&](int c, u32x4 (&kr)[8], u32x4 (&vr)[8]) {
-        const int tb = k0 + c * kChunk;
-        const int page = min(tb / a.block_size, a.bt_width - 1);
-        int64_t blk = btr[page];
-        blk = blk < 0 ? 0 : (blk >= a.n_blocks ? a.n_blocks - 1 : blk);
-        const int64_t base = blk * a.c_bs + head_off;
-        const int in_page = tb - (tb / a.block_size) * a.block_size;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int t = min(tb + 4 * i + ld_key, ri.lk - 1);
-            const int64_t off = base + static_cast<int64_t>(in_page + (t - tb)) * a.c_ts;
-            // streaming (non-temporal) loads: every K/V byte is read exactly once, so keep it out of the caches'
-            // normal replacement; measured ~15% more bandwidth than default loads on MI355X for this stream
-            kr[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.kc + off));
-            vr[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vc + off));
-        }
-    };
     // Registers -> the wave-private tiles. LDS executes one wave's accesses in issue order; the fences keep the
     // compiler from moving these stores above the previous chunk's reads.
     auto stage_chunk = [&](const u32x4 (&kr)[8], const u32x4 (&vr)[8]) {
@@ -279,11 +292,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
     __syncthreads();  // query tile staged
 
     // This wave's chunks are wave, wave + 4, ...; each one's K and V are in flight while the previous is processed.
-    {
-        u32x4 kr[8], vr[8];
-        if (wave < nch) load_chunk(wave, kr, vr);
-        for (int c = wave; c < nch; c += kWaves) process_chunk(c, kr, vr);
-    }
+    for (int c = wave; c < nch; c += kWaves) process_chunk(c, kr, vr);
 
     // ---- merge the 4 waves (fixed order, so the result does not depend on timing)
     const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -325,9 +334,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
         }
         __syncthreads();
     }
-    if (wave != kWaves - 1 || !qvalid) return;
-
     if (n_act == 1) {
+        if (wave != kWaves - 1 || !qvalid) return;
         const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
         uint16_t* op = a.out + static_cast<int64_t>(ri.q0 + qpos) * a.o_ts + static_cast<int64_t>(h) * a.o_hs;
 #pragma unroll
@@ -342,67 +350,115 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
                 *reinterpret_cast<u32x2*>(op + d) = u32x2{lo, hi};
             }
         }
-    } else {
-        const int64_t unit = (static_cast<int64_t>(r) * a.n_kv + g) * a.q_tiles + qt;
-        const int64_t pidx = unit * a.n_splits + s;
-        float* po = a.part_o + (pidx * kTileRows + nl) * kHeadDim;
+        return;
+    }
+
+    // Several splits. The partial (fp32 O and the per-row max and sum) is staged in LDS as [32 rows][128 dims] and
+    // written to the coherence point with device-scope stores, 512 contiguous bytes per wave instruction, so the
+    // unit's last split to finish reads it from any XCD.
+    const int64_t unit = (static_cast<int64_t>(r) * a.n_kv + g) * a.q_tiles + qt;
+    const int64_t pidx = unit * a.n_splits + s;
+    float* stage = reinterpret_cast<float*>(tiles) + kStageOffset;   // past the reduction buffer read above
+    float2* stage_ml = reinterpret_cast<float2*>(stage + kTileRows * kHeadDim);
+    if (wave == kWaves - 1) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
 #pragma unroll
             for (int jq = 0; jq < 4; ++jq) {
                 const int d = 32 * db + 8 * jq + 4 * gi;
-                *reinterpret_cast<float4*>(po + d) =
+                *reinterpret_cast<float4*>(stage + nl * kHeadDim + (d ^ ((nl & 7) << 2))) =
                     make_float4(o[db][4 * jq], o[db][4 * jq + 1], o[db][4 * jq + 2], o[db][4 * jq + 3]);
             }
         }
-        if (gi == 0) {
-            float* pm = a.part_ml + (pidx * kTileRows + nl) * 2;
-            pm[0] = m_all;
-            pm[1] = l_all;
+        if (gi == 0) stage_ml[nl] = make_float2(m_all, l_all);
+    }
+    __syncthreads();
+    {
+        uint64_t* po = reinterpret_cast<uint64_t*>(a.part_o + pidx * kTileRows * kHeadDim);
+#pragma unroll
+        for (int k = 0; k < kTileRows * kHeadDim / 2 / kThreads; ++k) {
+            const int e = tid + kThreads * k;          // u64 element of the [32][128] fp32 partial
+            const int row = e >> 6;
+            const int d = 2 * (e & 63);
+            const float2 v = *reinterpret_cast<const float2*>(stage + row * kHeadDim + (d ^ ((row & 7) << 2)));
+            __hip_atomic_store(po + e, static_cast<uint64_t>(__float_as_uint(v.x)) |
+                                           (static_cast<uint64_t>(__float_as_uint(v.y)) << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (tid < kTileRows) {
+            const float2 v = stage_ml[tid];
+            __hip_atomic_store(reinterpret_cast<uint64_t*>(a.part_ml) + pidx * kTileRows + tid,
+                               static_cast<uint64_t>(__float_as_uint(v.x)) |
+                                   (static_cast<uint64_t>(__float_as_uint(v.y)) << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-}
+    // vmcnt(0) in every wave: all of the workgroup's partial stores have completed before the count
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __shared__ int last_split;
+    __syncthreads();
+    if (tid == 0) {
+        const int before = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_split = (before == n_act - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!last_split) return;
 
-// Merge the split partials of every (row, kv head, query tile) that had more than one active split.
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    const int r = blockIdx.y;
-    const int g = blockIdx.x / a.q_tiles;
-    const int qt = blockIdx.x - g * a.q_tiles;
-    const RowInfo ri = row_info(a, r);
-    const int n_base = qt * kTileRows;
-    if (ri.lq <= 0 || n_base >= a.group * ri.lq) return;
-    const int n_act = active_splits(ri.lk, row_split_tokens(ri.lk, a.split_tokens, a.n_splits));
-    if (n_act <= 1) return;
-    const int64_t unit = (static_cast<int64_t>(r) * a.n_kv + g) * a.q_tiles + qt;
-    for (int e = threadIdx.x; e < kTileRows * kHeadDim / 4; e += blockDim.x) {
-        const int nl = e / (kHeadDim / 4);
-        const int d = (e - nl * (kHeadDim / 4)) * 4;
-        const int n = n_base + nl;
-        const int qpos = n / a.group;
-        if (qpos >= ri.lq || ri.q0 + qpos >= a.n_tokens || ri.q0 + qpos < 0) continue;
-        const int h = g * a.group + (n - qpos * a.group);
-        float m_all = -INFINITY;
-        for (int s = 0; s < n_act; ++s) m_all = fmaxf(m_all, a.part_ml[((unit * a.n_splits + s) * kTileRows + nl) * 2]);
-        const float m_use = (m_all == -INFINITY) ? 0.f : m_all;
-        float l_all = 0.f;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s = 0; s < n_act; ++s) {
-            const int64_t pidx = (unit * a.n_splits + s) * kTileRows + nl;
-            const float w = __builtin_amdgcn_exp2f(a.part_ml[pidx * 2] - m_use);
-            l_all += a.part_ml[pidx * 2 + 1] * w;
-            const float4 v = *reinterpret_cast<const float4*>(a.part_o + pidx * kHeadDim + d);
-            acc.x += v.x * w;
-            acc.y += v.y * w;
-            acc.z += v.z * w;
-            acc.w += v.w * w;
+    // The unit's last split merges all n_act partials in split order (the result does not depend on which split
+    // finished last). Every load is issued after this workgroup's own count returned, at the coherence point.
+    if (tid == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float2* ml = reinterpret_cast<float2*>(tiles);           // [n_act][32] (max, sum), then the split weights
+    float* inv_l = reinterpret_cast<float*>(ml + kMaxSplits * kTileRows);
+    const uint64_t* pml = reinterpret_cast<const uint64_t*>(a.part_ml) + unit * a.n_splits * kTileRows;
+    for (int e = tid; e < n_act * kTileRows; e += kThreads) {
+        const uint64_t v = __hip_atomic_load(pml + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ml[e] = make_float2(__uint_as_float(static_cast<uint32_t>(v)), __uint_as_float(static_cast<uint32_t>(v >> 32)));
+    }
+    __syncthreads();
+    if (tid < kTileRows) {
+        float m_u = -INFINITY;
+        for (int sp = 0; sp < n_act; ++sp) m_u = fmaxf(m_u, ml[sp * kTileRows + tid].x);
+        const float m_uu = (m_u == -INFINITY) ? 0.f : m_u;
+        float l_u = 0.f;
+        for (int sp = 0; sp < n_act; ++sp) {
+            const float w = __builtin_amdgcn_exp2f(ml[sp * kTileRows + tid].x - m_uu);
+            l_u += ml[sp * kTileRows + tid].y * w;
+            ml[sp * kTileRows + tid].x = w;   // the split's weight for this row
         }
-        const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
-        uint16_t* op = a.out + static_cast<int64_t>(ri.q0 + qpos) * a.o_ts + static_cast<int64_t>(h) * a.o_hs + d;
-        const uint32_t lo = nvs::float_to_bf16_bits(acc.x * inv) |
-                            (static_cast<uint32_t>(nvs::float_to_bf16_bits(acc.y * inv)) << 16);
-        const uint32_t hi = nvs::float_to_bf16_bits(acc.z * inv) |
-                            (static_cast<uint32_t>(nvs::float_to_bf16_bits(acc.w * inv)) << 16);
-        *reinterpret_cast<u32x2*>(op) = u32x2{lo, hi};
+        inv_l[tid] = l_u > 0.f ? 1.f / l_u : 0.f;
+    }
+    __syncthreads();
+    // thread -> u64 elements tid + 256 k (k < 8) of the [32][128] partials: rows tid / 64 + 4 k, dims 2 (tid % 64)
+    constexpr int kPer = kTileRows * kHeadDim / 2 / kThreads;
+    float acc[kPer][2];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) acc[k][0] = acc[k][1] = 0.f;
+    const uint64_t* pu = reinterpret_cast<const uint64_t*>(a.part_o) + unit * a.n_splits * kTileRows * kHeadDim / 2;
+    for (int sp = 0; sp < n_act; ++sp) {
+        uint64_t v[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
+            v[k] = __hip_atomic_load(pu + sp * (kTileRows * kHeadDim / 2) + tid + kThreads * k, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const float w = ml[sp * kTileRows + (tid >> 6) + 4 * k].x;
+            acc[k][0] += __uint_as_float(static_cast<uint32_t>(v[k])) * w;
+            acc[k][1] += __uint_as_float(static_cast<uint32_t>(v[k] >> 32)) * w;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int row = (tid >> 6) + 4 * k;
+        const int nm = n_base + row;
+        const int qpm = nm / a.group;
+        if (qpm >= ri.lq || ri.q0 + qpm >= a.n_tokens || ri.q0 + qpm < 0) continue;
+        const int hm = g * a.group + (nm - qpm * a.group);
+        const float inv = inv_l[row];
+        const uint32_t bits = nvs::float_to_bf16_bits(acc[k][0] * inv) |
+                              (static_cast<uint32_t>(nvs::float_to_bf16_bits(acc[k][1] * inv)) << 16);
+        *reinterpret_cast<uint32_t*>(a.out + static_cast<int64_t>(ri.q0 + qpm) * a.o_ts +
+                                     static_cast<int64_t>(hm) * a.o_hs + 2 * (tid & 63)) = bits;
     }
 }
 
@@ -418,25 +474,18 @@ SplitPlan plan_splits(int n_rows, int n_heads, int n_kv_heads, int max_seqlen_q,
     const int group = n_heads / n_kv_heads;
     p.q_tiles = (group * max_seqlen_q + kTileRows - 1) / kTileRows;
     const int64_t units = static_cast<int64_t>(n_rows) * n_kv_heads * p.q_tiles;
-    // One resident round of workgroups: 256 CUs x 2 workgroups (the kernel's occupancy). Rows are only split
-    // when the (row, kv head, tile) units alone leave a large part of that round empty: a split costs a combine
-    // pass and shortens each wave's stream, which measured slower than an unsplit grid that nearly fills a round.
-    int64_t target = 512;
-    if (const char* env = std::getenv("NVS_ATTN_TARGET_WGS")) {
-        const long v = std::strtol(env, nullptr, 10);
-        if (v > 0) target = v;
-    }
+    // One resident round of workgroups: 256 CUs x 2 workgroups (the kernel's occupancy). Keys are split only when
+    // the (row, kv head, tile) units fill less than half of that round, and then into enough splits to fill it:
+    // measured on batch-8/16/32 verify layers (3k contexts), a split costs its partial and the merge, which a grid
+    // of one unsplit workgroup per CU does not win back, while a grid under one workgroup per CU does.
+    constexpr int64_t kRound = 512;
     int64_t want = 1;
-    if (units > 0 && units * 10 < target * 9) want = (target + units - 1) / units;
+    if (units > 0 && units * 2 < kRound) want = (kRound + units - 1) / units;
     const int64_t max_k = max_seqlen_k > 0 ? max_seqlen_k : 1;
     int64_t ts = (max_k + want - 1) / want;
-    int64_t min_ts = 2 * kSplitQuantum;
-    if (const char* env = std::getenv("NVS_ATTN_MIN_SPLIT")) {
-        const long v = std::strtol(env, nullptr, 10);
-        if (v > 0) min_ts = v;
-    }
+    int64_t min_ts = 2 * kSplitQuantum;   // a row's split holds at least this many keys (the device sizes them)
+    if (ts * kMaxSplits < max_k) ts = (max_k + kMaxSplits - 1) / kMaxSplits;   // at most kMaxSplits splits
     ts = (ts + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum;
-    min_ts = (min_ts + kChunk - 1) / kChunk * kChunk;
     if (ts < min_ts) ts = min_ts;
     // The grid has n_splits splits per unit, from max_seqlen_k; each row spreads its own keys over them on the
     // device, at least split_tokens per split.
@@ -482,7 +531,8 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_token_stride, int64_
                                    const int32_t* context_lens, int query_len_per_seq, int n_rows, int max_seqlen_q,
                                    int max_seqlen_k, int n_heads, int n_kv_heads, int head_dim, int block_size,
                                    float scale, int causal, int dtype, void* out, int64_t out_token_stride,
-                                   int64_t out_head_stride, void* workspace, size_t workspace_bytes, void* stream) {
+                                   int64_t out_head_stride, int32_t* unit_counters, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
     nvs::clear_error();
     int st = validate_sizes(n_rows, n_heads, n_kv_heads, head_dim, max_seqlen_q, max_seqlen_k);
     if (st != NVS_OK) return st;
@@ -517,6 +567,8 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_token_stride, int64_
     NVS_CHECK(plan.workspace == 0 || (workspace != nullptr && workspace_bytes >= plan.workspace),
               NVS_ERR_WORKSPACE, "paged_attention: workspace of %zu bytes needed, %zu given", plan.workspace,
               workspace_bytes);
+    NVS_CHECK(plan.n_splits == 1 || unit_counters != nullptr, NVS_ERR_INVALID,
+              "paged_attention: this plan splits keys and needs unit_counters");
     NVS_CHECK(static_cast<int64_t>(n_kv_heads) * plan.q_tiles <= 65535 && n_rows <= 65535, NVS_ERR_UNSUPPORTED,
               "paged_attention: grid too large (rows %d, kv heads x tiles %lld)", n_rows,
               (long long)n_kv_heads * plan.q_tiles);
@@ -555,18 +607,13 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_token_stride, int64_
                                               : 0;
     a.part_o = plan.n_splits > 1 ? reinterpret_cast<float*>(ws) : nullptr;
     a.part_ml = plan.n_splits > 1 ? reinterpret_cast<float*>(ws + po_bytes) : nullptr;
+    a.counters = unit_counters;
     a.n_splits = plan.n_splits;
     a.split_tokens = plan.split_tokens;
     a.q_tiles = plan.q_tiles;
 
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(plan.n_splits, n_kv_heads * plan.q_tiles, n_rows);
+    const dim3 grid(n_kv_heads * plan.q_tiles, n_rows, plan.n_splits);
     hipLaunchKernelGGL(attn_split_kernel, grid, dim3(kThreads), 0, s, a);
-    st = nvs::check_launch("paged_attention split kernel");
-    if (st != NVS_OK) return st;
-    if (plan.n_splits > 1) {
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(n_kv_heads * plan.q_tiles, n_rows), dim3(256), 0, s, a);
-        st = nvs::check_launch("paged_attention combine kernel");
-    }
-    return st;
+    return nvs::check_launch("paged_attention split kernel");
 }

@@ -56,7 +56,7 @@ struct PosRecord {
 static_assert(sizeof(PosRecord) == 32, "record layout");
 
 // The race of a batch row whose tail position does not truncate, handed by the accept kernel's row finish to
-// dense_race_chunk_kernel / dense_race_merge_kernel (used when no row truncates, so the host launches them).
+// dense_race_chunk_kernel (used when no row truncates, so the host launches it after the accept kernel).
 struct DenseRace {
     int64_t pos;     // logit row of the position after the accepted prefix
     int64_t qrow;    // q row b * k + min(n, k - 1); -1 for the bonus position (w = p)
@@ -790,6 +790,31 @@ __device__ __forceinline__ bool count_position(int* counter, int64_t n_positions
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): every store of this wave has completed
     const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return before == static_cast<int>(n_positions) - 1;
+}
+
+// The end of one vocabulary chunk of a race spread over (row, chunk) workgroups, run by wave 0 of the chunk's
+// workgroup: lane 0 publishes the chunk's best key to the row's partials at the coherence point and counts the
+// chunk on the row's counter (count_position); the workgroup that counts last reads every chunk's key of the row
+// (one load per lane, at the coherence point), resets the counter for the next call and returns true with the
+// row's best key in winner. Every lane of wave 0 must call it; the result is uniform over the wave.
+__device__ __forceinline__ bool finish_race_chunk(uint64_t* row_partials, int n_chunks, int c, uint64_t key,
+                                                  int* counter, uint64_t& winner) {
+    const int lane = threadIdx.x & 63;
+    int last = 0;
+    if (lane == 0) {
+        __hip_atomic_store(row_partials + c, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = count_position(counter, n_chunks) ? 1 : 0;
+    }
+    last = __builtin_amdgcn_readfirstlane(last);
+    if (!last) return false;
+    uint64_t best = 0;
+    for (int j = lane; j < n_chunks; j += 64) {
+        const uint64_t v = __hip_atomic_load(row_partials + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        best = best > v ? best : v;
+    }
+    winner = wave_max_u64(best);
+    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
 }
 
 // ---------------------------------------------------------------- q as candidate rows
@@ -2255,6 +2280,7 @@ struct RaceArgs {
     int64_t vocab;
     int n_chunks;
     uint64_t* partial;  // [rows, n_chunks]
+    int* counters;      // [rows] chunks of the row finished; zero between calls
     int64_t* n_accept;
     int64_t* out;
 };
@@ -2369,23 +2395,16 @@ __global__ __launch_bounds__(256) void race_chunk_kernel(RaceArgs a) {
     best = wave_max_u64(best);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 64) {
+        // the row's last chunk to finish picks the winner over the row's chunk keys (the accepted prefix was
+        // written by the row's chunk 0)
         uint64_t all = 0;
         for (int w = 0; w < 4; ++w) all = red[w] > all ? red[w] : all;
-        a.partial[r * a.n_chunks + c] = all;
+        uint64_t win = 0;
+        if (finish_race_chunk(a.partial + r * a.n_chunks, a.n_chunks, c, all, a.counters + r, win) &&
+            threadIdx.x == 0)
+            a.out[r] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(win));
     }
-}
-
-// Winner of each row over its chunk partials (the accepted prefix was written by the row's chunk 0).
-__global__ __launch_bounds__(64) void race_merge_kernel(RaceArgs a) {
-    const int64_t r = blockIdx.x;
-    uint64_t best = 0;
-    for (int c = threadIdx.x; c < a.n_chunks; c += 64) {
-        const uint64_t v = a.partial[r * a.n_chunks + c];
-        best = best > v ? best : v;
-    }
-    best = wave_max_u64(best);
-    if (threadIdx.x == 0) a.out[r] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
 }
 
 // ---------------------------------------------------------------- greedy
@@ -2719,13 +2738,13 @@ extern "C" int nvs_race_workspace_size(int64_t n_rows, int64_t vocab, size_t* by
 }
 
 extern "C" int nvs_race(const float* weights, int64_t weights_row_stride, const float* noise,
-                        int64_t noise_row_stride, int64_t n_rows, int64_t vocab, int64_t* out, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+                        int64_t noise_row_stride, int64_t n_rows, int64_t vocab, int64_t* out,
+                        int32_t* row_counters, void* workspace, size_t workspace_bytes, void* stream) {
     nvs::clear_error();
     NVS_CHECK(n_rows >= 0 && vocab > 0 && vocab < 0x7fffffffLL, NVS_ERR_INVALID, "race: bad sizes");
     NVS_CHECK(n_rows <= 0x7fffffffLL, NVS_ERR_UNSUPPORTED, "race: too many rows");
     if (n_rows == 0) return NVS_OK;
-    NVS_CHECK(weights && noise && out, NVS_ERR_INVALID, "race: null pointer");
+    NVS_CHECK(weights && noise && out && row_counters, NVS_ERR_INVALID, "race: null pointer");
     // stride 0 = one row broadcast over all rows (an expanded tensor)
     NVS_CHECK((weights_row_stride == 0 || weights_row_stride >= vocab) &&
                   (noise_row_stride == 0 || noise_row_stride >= vocab),
@@ -2743,6 +2762,7 @@ extern "C" int nvs_race(const float* weights, int64_t weights_row_stride, const 
     a.vocab = vocab;
     a.n_chunks = static_cast<int>(race_chunks(vocab));
     a.partial = static_cast<uint64_t*>(workspace);
+    a.counters = row_counters;
     a.out = out;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool vec = vocab % 4 == 0 && nvs::aligned16(weights) && nvs::aligned16(noise) &&
@@ -2752,10 +2772,7 @@ extern "C" int nvs_race(const float* weights, int64_t weights_row_stride, const 
     } else {
         hipLaunchKernelGGL((race_chunk_kernel<false, false>), dim3(n_rows, a.n_chunks), dim3(256), 0, s, a);
     }
-    int st = nvs::check_launch("race chunk kernel");
-    if (st != NVS_OK) return st;
-    hipLaunchKernelGGL(race_merge_kernel, dim3(n_rows), dim3(64), 0, s, a);
-    return nvs::check_launch("race merge kernel");
+    return nvs::check_launch("race chunk kernel");
 }
 
 extern "C" int nvs_accept_random_workspace_size(int64_t batch, int64_t vocab, size_t* bytes) {
@@ -2774,13 +2791,13 @@ static int accept_common_checks(const int64_t* drafts, int64_t batch, int num_dr
 
 extern "C" int nvs_accept_random(const float* p, const float* q, const int64_t* drafts, const int64_t* verified_lens,
                                  const float* uniforms, const float* noise, int64_t batch, int num_drafts,
-                                 int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail, void* workspace,
-                                 size_t workspace_bytes, void* stream) {
+                                 int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail,
+                                 int32_t* row_counters, void* workspace, size_t workspace_bytes, void* stream) {
     nvs::clear_error();
     int st = accept_common_checks(drafts, batch, num_drafts, n_pos, vocab, n_accept, tail);
     if (st != NVS_OK) return st;
     if (batch == 0) return NVS_OK;
-    NVS_CHECK(p && q && uniforms && noise, NVS_ERR_INVALID, "accept_random: null pointer");
+    NVS_CHECK(p && q && uniforms && noise && row_counters, NVS_ERR_INVALID, "accept_random: null pointer");
     NVS_CHECK(verified_lens != nullptr || n_pos == batch * (num_drafts + 1), NVS_ERR_INVALID,
               "accept_random: p has %lld positions, expected batch*(k+1) = %lld", (long long)n_pos,
               (long long)(batch * (num_drafts + 1)));
@@ -2803,6 +2820,7 @@ extern "C" int nvs_accept_random(const float* p, const float* q, const int64_t* 
     a.vocab = vocab;
     a.n_chunks = static_cast<int>(race_chunks(vocab));
     a.partial = static_cast<uint64_t*>(workspace);
+    a.counters = row_counters;
     a.n_accept = n_accept;
     a.out = tail;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -2812,10 +2830,7 @@ extern "C" int nvs_accept_random(const float* p, const float* q, const int64_t* 
     } else {
         hipLaunchKernelGGL((race_chunk_kernel<true, false>), dim3(batch, a.n_chunks), dim3(256), 0, s, a);
     }
-    st = nvs::check_launch("accept_random chunk kernel");
-    if (st != NVS_OK) return st;
-    hipLaunchKernelGGL(race_merge_kernel, dim3(batch), dim3(64), 0, s, a);
-    return nvs::check_launch("accept_random merge kernel");
+    return nvs::check_launch("accept_random chunk kernel");
 }
 
 extern "C" int nvs_accept_greedy_workspace_size(int64_t n_pos, int64_t vocab, size_t* bytes) {
@@ -2886,8 +2901,9 @@ __global__ __launch_bounds__(256) void dense_race_chunk_kernel(SelArgs a) {
     const int64_t r = blockIdx.x;
     const int c = blockIdx.y;
     const DenseRace d = a.dense_race[r];
+    if (!d.valid) return;   // the row's tail is its position's own race, already written (uniform per row)
     uint64_t best = 0;
-    if (d.valid) {
+    {
         const int64_t i0 = static_cast<int64_t>(c) * kRaceChunk;
         const int64_t i1 = min(i0 + kRaceChunk, a.vocab);
         const float* erow = a.noise + r * a.vocab;
@@ -2947,23 +2963,15 @@ __global__ __launch_bounds__(256) void dense_race_chunk_kernel(SelArgs a) {
     best = wave_max_u64(best);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 64) {
+        // the row's counter was left at zero by the accept kernel's row finish; the row's last chunk writes the tail
         uint64_t all = 0;
         for (int w = 0; w < 4; ++w) all = red[w] > all ? red[w] : all;
-        a.dense_partial[r * a.dense_chunks + c] = all;
+        uint64_t win = 0;
+        if (finish_race_chunk(a.dense_partial + r * a.dense_chunks, a.dense_chunks, c, all, a.counters + r, win) &&
+            threadIdx.x == 0)
+            a.tail[r] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(win));
     }
-}
-
-__global__ __launch_bounds__(64) void dense_race_merge_kernel(SelArgs a) {
-    const int64_t r = blockIdx.x;
-    if (!a.dense_race[r].valid) return;   // the row's tail is its position's own race, already written
-    uint64_t best = 0;
-    for (int c = threadIdx.x; c < a.dense_chunks; c += 64) {
-        const uint64_t v = a.dense_partial[r * a.dense_chunks + c];
-        best = best > v ? best : v;
-    }
-    best = wave_max_u64(best);
-    if (threadIdx.x == 0) a.tail[r] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
 }
 
 // Workspace of the fused accept: the position records, then (no truncating row) the dense races and their chunks.
@@ -3069,10 +3077,7 @@ static int spec_accept_impl(const void* logits, int logits_dtype, int64_t logits
         if (vec) hipLaunchKernelGGL((dense_race_chunk_kernel<NVS_DTYPE_F16, true>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((dense_race_chunk_kernel<NVS_DTYPE_F16, false>), grid, dim3(256), 0, s, a);
     }
-    st = nvs::check_launch("spec_accept dense race");
-    if (st != NVS_OK) return st;
-    hipLaunchKernelGGL(dense_race_merge_kernel, dim3(static_cast<unsigned>(batch)), dim3(64), 0, s, a);
-    return nvs::check_launch("spec_accept dense race merge");
+    return nvs::check_launch("spec_accept dense race");
 }
 
 extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_stride,

@@ -67,6 +67,11 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
                "store_kvcache")
 
 
+# The split merge's per-unit counters are kept in one zero-filled buffer per device, sized for at least this many
+# (row, kv head, query tile) units so that graphs captured after smaller eager calls still fit in it.
+_MIN_COUNTER_UNITS = 65536
+
+
 def _paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_table: torch.Tensor,
                      cu_seqlens_q: torch.Tensor | None, cu_seqlens_k: torch.Tensor | None,
                      context_lens: torch.Tensor | None, query_len_per_seq: int, num_rows: int, max_seqlen_q: int,
@@ -100,13 +105,18 @@ def _paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                "paged_attention_workspace_size")
     ws = workspace if workspace is not None and workspace.numel() >= nbytes.value else \
         _lib.workspace(nbytes.value, q.device)
+    # a plan that splits keys merges them in the launch: per-unit counters, zero between calls
+    counters = None
+    if nbytes.value > 0:
+        units = num_rows * Hkv * -(-(H // Hkv) * max_seqlen_q // 32)
+        counters = _lib.persistent_workspace("attention_unit_counters", 4 * max(units, _MIN_COUNTER_UNITS), q.device)
     _lib.check(lib.nvs_paged_attention(
         q.data_ptr(), q.stride(0), q.stride(1), T, k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), block_table.data_ptr(), block_table.stride(0),
         block_table.shape[1], _lib.ptr(cu_seqlens_q), _lib.ptr(cu_seqlens_k), _lib.ptr(context_lens), query_len_per_seq,
         num_rows, max_seqlen_q, max_seqlen_k, H, Hkv, D, block_size, float(softmax_scale), int(bool(causal)),
-        _lib.dtype_code(q.dtype), out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(ws), nbytes.value,
-        _lib.stream_of(q)),
+        _lib.dtype_code(q.dtype), out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(counters), _lib.ptr(ws),
+        nbytes.value, _lib.stream_of(q)),
         "paged_attention")
     return out
 

@@ -144,6 +144,15 @@ def exponential_noise_(out: torch.Tensor, generator: torch.Generator | None) -> 
     return out.exponential_(1.0, generator=generator).clamp_min_(EXPONENTIAL_NOISE_FLOOR)
 
 
+# Row counters of the one-launch races: int32 per row, zero between calls (each call leaves them zero). Sized for
+# at least this many rows so that a graph captured after a smaller eager call still finds a large enough buffer.
+_MIN_COUNTER_ROWS = 16384
+
+
+def _row_counters(name: str, n_rows: int, device: torch.device) -> torch.Tensor:
+    return _lib.persistent_workspace(name, 4 * max(n_rows, _MIN_COUNTER_ROWS), device)
+
+
 def race(weights: torch.Tensor, noise: torch.Tensor) -> torch.Tensor:
     """argmax(w / E) over the last dim, first index on ties (spec_sampler.py:104-106)."""
     _lib.require_device(weights, noise)
@@ -160,8 +169,9 @@ def race(weights: torch.Tensor, noise: torch.Tensor) -> torch.Tensor:
     nbytes = _lib.size_out()
     _lib.check(lib.nvs_race_workspace_size(n_rows, vocab, ctypes.byref(nbytes)), "race_workspace_size")
     ws = _lib.workspace(nbytes.value, weights.device)
+    counters = _row_counters("race_row_counters", n_rows, weights.device)
     _lib.check(lib.nvs_race(w.data_ptr(), w_stride, e.data_ptr(), e_stride, n_rows, vocab, out.data_ptr(),
-                            _lib.ptr(ws), nbytes.value, _lib.stream_of(weights)),
+                            counters.data_ptr(), _lib.ptr(ws), nbytes.value, _lib.stream_of(weights)),
                "race")
     return out.view(lead)
 
@@ -214,10 +224,11 @@ def _accept_random(p, q, drafts, verified_lens, generator):
     _lib.check(lib.nvs_accept_random_workspace_size(batch_size, vocab, ctypes.byref(nbytes)),
                "accept_random_workspace_size")
     ws = _lib.workspace(nbytes.value, p.device)
+    counters = _row_counters("accept_random_row_counters", batch_size, p.device)
     _lib.check(lib.nvs_accept_random(p.data_ptr(), q.data_ptr(), drafts_c.data_ptr(), _lib.ptr(lens),
                                      uniforms.data_ptr(), noise.data_ptr(), batch_size, num_drafts, p.shape[0], vocab,
-                                     n_accept.data_ptr(), tail.data_ptr(), _lib.ptr(ws), nbytes.value,
-                                     _lib.stream_of(p)),
+                                     n_accept.data_ptr(), tail.data_ptr(), counters.data_ptr(), _lib.ptr(ws),
+                                     nbytes.value, _lib.stream_of(p)),
                "accept_random")
     return n_accept, tail
 
@@ -361,8 +372,10 @@ def accept_random_with_draws(p: torch.Tensor, q: torch.Tensor, drafts: torch.Ten
     _lib.check(lib.nvs_accept_random_workspace_size(batch_size, vocab, ctypes.byref(nbytes)),
                "accept_random_workspace_size")
     ws = _lib.workspace(nbytes.value, p.device)
+    counters = _row_counters("accept_random_row_counters", batch_size, p.device)
     _lib.check(lib.nvs_accept_random(p.data_ptr(), q.data_ptr(), drafts_c.data_ptr(), _lib.ptr(lens), u.data_ptr(),
                                      e.data_ptr(), batch_size, num_drafts, p.shape[0], vocab, n_accept.data_ptr(),
-                                     tail.data_ptr(), _lib.ptr(ws), nbytes.value, _lib.stream_of(p)),
+                                     tail.data_ptr(), counters.data_ptr(), _lib.ptr(ws), nbytes.value,
+                                     _lib.stream_of(p)),
                "accept_random")
     return n_accept, tail

@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version_and_empty_error(lib):
-    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 6
+    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 7
     assert isinstance(lib.nvs_last_error(), bytes)
 
 
@@ -47,7 +47,8 @@ def attn_args(**over):
     args = dict(q=1 << 20, q_ts=4096, q_hs=128, n_tokens=8, k=1 << 21, v=1 << 22, cache_blocks=4, c_bs=262144,
                 c_ts=1024, c_hs=128, bt=1 << 23, bt_rs=4, bt_width=4, cu_q=1 << 24, cu_k=1 << 25, ctx=None,
                 qlen=0, rows=1, mq=8, mk=1024, h=32, hkv=8, d=128, bs=256, scale=0.088, causal=1,
-                dtype=_lib.DTYPE_BF16, out=1 << 26, o_ts=4096, o_hs=128, ws=None, ws_bytes=0, stream=None)
+                dtype=_lib.DTYPE_BF16, out=1 << 26, o_ts=4096, o_hs=128, counters=None, ws=None, ws_bytes=0,
+                stream=None)
     args.update(over)
     return list(args.values())
 
@@ -64,6 +65,7 @@ def attn_args(**over):
     (dict(scale=0.0), _lib.NVS_ERR_INVALID),
     (dict(bt_width=0), _lib.NVS_ERR_INVALID),
     (dict(rows=1, mk=4096), _lib.NVS_ERR_WORKSPACE),   # one row: the plan splits its keys, partials needed
+    (dict(rows=1, mk=4096, ws=1 << 27, ws_bytes=1 << 30), _lib.NVS_ERR_INVALID),   # and the merge's counters
 ])
 def test_attention_rejects_bad_arguments_without_launching(lib, over, status):
     assert lib.nvs_paged_attention(*attn_args(**over)) == status
@@ -78,6 +80,14 @@ def test_attention_workspace_plan(lib):
     # batch 2: the keys are split to fill the chip, partials need a workspace
     assert lib.nvs_paged_attention_workspace_size(2, 32, 8, 128, 8, 4096, ctypes.byref(n)) == 0
     assert n.value > 0
+    # batch 32 (256 units, one per CU) stays unsplit; batch 16 (128 units) is split
+    assert lib.nvs_paged_attention_workspace_size(32, 32, 8, 128, 8, 4096, ctypes.byref(n)) == 0
+    assert n.value == 0
+    assert lib.nvs_paged_attention_workspace_size(16, 32, 8, 128, 8, 4096, ctypes.byref(n)) == 0
+    assert n.value > 0
+    # at most 64 splits per unit whatever max_seqlen_k: partials of 32 rows x (128 + 2) fp32 per split
+    assert lib.nvs_paged_attention_workspace_size(1, 32, 8, 128, 8, 1 << 17, ctypes.byref(n)) == 0
+    assert 0 < n.value <= 8 * 64 * 32 * 130 * 4 + 256
     small = ctypes.c_size_t()
     assert lib.nvs_paged_attention_workspace_size(1, 32, 8, 128, 8, 64, ctypes.byref(small)) == 0
     assert small.value == 0            # 64 keys: one split, no partials
@@ -99,7 +109,12 @@ def test_sampler_rejects_bad_arguments_without_launching(lib):
     assert st == _lib.NVS_ERR_WORKSPACE
     assert lib.nvs_probs_from_logits(1 << 20, 9, 100, 4, 100, 1, 1 << 20, None, None, 0, 0, 1 << 20, None, 0,
                                      None) == _lib.NVS_ERR_INVALID
-    assert lib.nvs_race(1 << 20, 10, 1 << 20, 10, 3, 100, 1 << 20, None, 0, None) == _lib.NVS_ERR_INVALID
+    assert lib.nvs_race(1 << 20, 10, 1 << 20, 10, 3, 100, 1 << 20, 1 << 20, None, 0, None) == _lib.NVS_ERR_INVALID
+    # the one-launch race needs its zeroed row counters
+    assert lib.nvs_race(1 << 20, 100, 1 << 20, 100, 3, 100, 1 << 20, None, 1 << 20, 1 << 20,
+                        None) == _lib.NVS_ERR_INVALID
+    assert lib.nvs_accept_random(1 << 20, 1 << 20, 1 << 20, None, 1 << 20, 1 << 20, 2, 3, 8, 100, 1 << 20, 1 << 20,
+                                 None, 1 << 20, 1 << 20, None) == _lib.NVS_ERR_INVALID
 
 
 def test_store_kvcache_rejects_bad_arguments(lib):

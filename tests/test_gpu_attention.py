@@ -9,6 +9,7 @@ import torch
 
 import nvs_amd.workloads as wl
 from conftest import log_case
+from nvs_amd import _lib
 from nvs_amd.layers import attention as nattn
 from nvs_amd.utils.context import reset_context, set_context
 from oracle import attention as ref
@@ -70,9 +71,24 @@ def test_rows_with_no_queries_and_graph_sized_bounds(device):
 
 
 def test_long_context_splits(device):
+    """Two rows split over many key ranges: each unit's last split to finish merges the partials in the launch,
+    and leaves the unit counters at zero for the next call."""
     log_case("attention long context 4096 split-K")
     c = wl.verify_attention_case([8, 4], [4096, 3001], 32, 8, 128)
     check(run_varlen(c, device), c)
+    c = wl.verify_attention_case([1], [4000], 32, 8, 128)
+    check(run_varlen(c, device), c)
+    counters = _lib.persistent_workspace("attention_unit_counters", 4, torch.device(device))
+    torch.cuda.synchronize()
+    assert int(counters.view(torch.int32).abs().sum()) == 0
+
+
+def test_sixty_two_splits_of_one_long_row(device):
+    """One 16,000-key row planned for 32k keys: 8 units, so the plan takes its 64-split maximum and the row is cut
+    into 62 equal splits, all merged by the last one to finish."""
+    log_case("attention one row, 16000 keys, max_seqlen_k 32768 (62 splits)")
+    c = wl.verify_attention_case([3], [16000], 32, 8, 128, pad_tokens_to=1)
+    check(run_varlen(c, device, max_seqlen_k=32768), c)
 
 
 def test_c3_full_size(device):

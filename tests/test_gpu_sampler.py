@@ -16,6 +16,7 @@ import torch
 import known_answers as ka
 import nvs_amd.workloads as wl
 from conftest import log_case
+from nvs_amd import _lib
 from nvs_amd.layers import spec_sampler as ns
 from oracle import spec_sampler as ref
 
@@ -92,6 +93,52 @@ def test_race_ties_zero_weights_and_random_rows(device):
     w[w < 0.5] = 0
     e = torch.empty(33, 70000).exponential_(generator=gen).clamp_min_(1e-10)
     assert torch.equal(ns.race(w.to(device), e.to(device)).cpu(), ref.race(w, e))
+
+
+def test_one_launch_races_leave_their_counters_at_zero(device):
+    """race and accept_random pick each row's winner in the workgroup of the row's last chunk to finish, counting
+    chunks on a zero-filled per-row counter that every call leaves at zero: calls of different sizes in a row and
+    HIP-graph replays (with eager calls between them) all give the oracle's answer."""
+    log_case("race / accept_random counters across calls and graph replays")
+    gen = torch.Generator().manual_seed(11)
+    cases = []
+    for rows in (40, 7, 40):
+        w = torch.rand(rows, 50000, generator=gen)
+        w[w < 0.3] = 0
+        e = torch.empty(rows, 50000).exponential_(generator=gen).clamp_min_(1e-10)
+        cases.append((w.to(device), e.to(device), ref.race(w, e)))
+    for w, e, want in cases:
+        assert torch.equal(ns.race(w, e).cpu(), want)
+    counters = _lib.persistent_workspace("race_row_counters", 4, torch.device(device))
+    torch.cuda.synchronize()
+    assert int(counters.view(torch.int32).abs().sum()) == 0
+    w, e, want = cases[0]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ns.race(w, e)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = ns.race(w, e)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), want)
+        assert torch.equal(ns.race(cases[1][0], cases[1][1]).cpu(), cases[1][2])   # eager work between replays
+    case = wl.sampler_case(8, 7, 50000, verified_lens=[1, 8, 3, 5, 2, 7, 4, 6], draft_probs_fn=draft_probs)
+    lens = case.verified_lens
+    p = ref.probs_from_logits(case.logits, case.temperatures.repeat_interleave(lens),
+                              case.top_k.repeat_interleave(lens), case.top_p.repeat_interleave(lens),
+                              case.max_top_k, case.has_top_p)
+    want = ref.accept_random_varlen(p, case.q, case.drafts, lens, case.uniforms, case.noise)
+    for _ in range(3):
+        got = ns.accept_random_with_draws(p.to(device), case.q.to(device), case.drafts.to(device), lens.to(device),
+                                          case.uniforms.to(device), case.noise.to(device))
+        assert torch.equal(got[0].cpu(), want[0]) and torch.equal(got[1].cpu(), want[1])
+    counters = _lib.persistent_workspace("accept_random_row_counters", 4, torch.device(device))
+    torch.cuda.synchronize()
+    assert int(counters.view(torch.int32).abs().sum()) == 0
 
 
 def test_sample_frequencies_follow_the_weights(device):
