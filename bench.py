@@ -96,6 +96,7 @@ def attention_bench(args, dev):
         log(f"[bench] attention ({layout} cache): {ms * 1e3:.1f} us/layer, {gbs:.0f} GB/s = "
             f"{100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
         timed[layout] = (ms, gbs)
+        hip_out = out.float().cpu()   # the last timed launch's output (both layouts give the same bits)
         del g, out
     ms, gbs = timed["head_major"]
     tm_ms, tm_gbs = timed["token_major"]
@@ -103,7 +104,7 @@ def attention_bench(args, dev):
                    "kv_layout": "token_major [blocks, 256, 8, 128] (the reference's)", "us": round(tm_ms * 1e3, 2),
                    "GBs": round(tm_gbs, 1), "frac": round(tm_gbs / HBM_PEAK_GBS, 4),
                    "traffic": MEASURED_TRAFFIC["verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_token_major"]}
-    return case, ms, kv + qo, gbs, flops, token_major
+    return case, ms, kv + qo, gbs, flops, token_major, hip_out
 
 
 def launch_bound_bench(args, dev):
@@ -217,11 +218,40 @@ def sampler_bench(args, dev):
         "greedy_fp32": {"us": round(msg * 1e3, 2), "GBs": round(alg / (msg * 1e-3) / 1e9, 1),
                         "algorithmic_bytes": alg, "kernel": "argmax_kernel + greedy_finalize_kernel"},
     }
-    return {"workload": "spec_accept_b64_k7_v151936_fp32_topk64", "us": round(ms * 1e3, 2), "variants": variants,
-            "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": alg,
-            "traffic": MEASURED_TRAFFIC["spec_accept_b64_k7_v151936_fp32_topk64"],
-            "kernel": "select_kernel<f32, accept> (one launch per call)",
-            "mean_accepted": round(float(n.float().mean()), 3)}
+    out = {"workload": "spec_accept_b64_k7_v151936_fp32_topk64", "us": round(ms * 1e3, 2), "variants": variants,
+           "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": alg,
+           "traffic": MEASURED_TRAFFIC["spec_accept_b64_k7_v151936_fp32_topk64"],
+           "kernel": "select_kernel<f32, accept> (one launch per call)",
+           "mean_accepted": round(float(n.float().mean()), 3)}
+    if args.cpu_baseline == "on":
+        out["cpu_baseline"] = sampler_cpu_baseline(case, n.cpu(), tail.cpu())
+    return out
+
+
+def sampler_cpu_baseline(case, n_gpu, tail_gpu):
+    """The torch-CPU restatement of the reference's sampler path (oracle: probs_from_logits then
+    accept_random, the two calls of SpeculativeDecoder._accept) over the whole 64 x 8 x 151,936 case on the host
+    cores, with the GPU run's uniforms and noise; its decisions are compared with the fused kernel's."""
+    import torch
+
+    from oracle import spec_sampler as ref
+    torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+
+    def run():
+        return ref.accept_from_logits(case.logits, case.q, case.drafts, case.temperatures, case.top_k, case.top_p,
+                                      case.max_top_k, case.has_top_p, None, case.uniforms, case.noise)
+
+    n_cpu, tail_cpu = run()
+    same = bool(torch.equal(n_cpu, n_gpu) and torch.equal(tail_cpu, tail_gpu))
+    sec, runs = time_cpu(run)
+    T, V = case.logits.shape
+    gbs = T * V * 4 / sec / 1e9
+    log(f"[bench] sampler cpu baseline: {sec * 1e3:.1f} ms per call on {torch.get_num_threads()} threads "
+        f"(same decisions as the GPU: {same})")
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"the whole 64 x 8 x 151,936 fp32 case (probs_from_logits + accept_random, same draws), "
+                      f"median of {runs} runs: {sec * 1e3:.1f} ms per call", "ms_per_call": round(sec * 1e3, 2),
+            "same_decisions_as_gpu": same}
 
 
 def draft_block_bench(args, dev):
@@ -562,9 +592,11 @@ def copy_probe(args, dev):
     return {"bytes_read": n, "bytes_written": n, "us": round(ms * 1e3, 2), "GBs_read_plus_write": round(gbs, 1)}
 
 
-def cpu_baseline(case):
+def cpu_baseline(case, hip_out):
     """The torch-CPU restatement of the reference's paged attention (oracle), in fp32 on the host cores, over the
-    whole batch-64 layer (inputs converted to fp32 before timing)."""
+    whole batch-64 layer (inputs converted to fp32 before timing). Also the numerics beside it: the GPU output
+    against the CPU path over every row, and both against the fp64 brute force on the layer's first four rows."""
+    import numpy as np
     import torch
 
     from oracle import attention as ref
@@ -573,16 +605,38 @@ def cpu_baseline(case):
     kc = case.k_cache.float()
     vc = case.v_cache.float()
     rows = case.rows
+    got = {}
 
     def run():
-        ref.paged_attention_t32(q, kc, vc, case.block_tables, rows, case.scale, True)
+        got["t32"] = ref.paged_attention_t32(q, kc, vc, case.block_tables, rows, case.scale, True)
 
     sec, runs = time_cpu(run)
     gbs = (case.kv_bytes() + case.qo_bytes()) / sec / 1e9
     log(f"[bench] cpu baseline: {sec * 1e3:.1f} ms/layer on {torch.get_num_threads()} threads")
+    # fp64 brute force on the first four rows, their pages gathered into a compact cache
+    bs = case.k_cache.shape[1]
+    sub = rows[:4]
+    pages = [(lk + bs - 1) // bs for _, _, lk in sub]
+    blocks = sorted({int(b) for r, n in enumerate(pages) for b in case.block_tables[r, :n]})
+    remap = {b: i for i, b in enumerate(blocks)}
+    tables = torch.zeros(len(sub), max(pages), dtype=torch.int32)
+    for r, n in enumerate(pages):
+        tables[r, :n] = torch.tensor([remap[int(b)] for b in case.block_tables[r, :n]], dtype=torch.int32)
+    want = ref.paged_attention_f64(case.q, case.k_cache[blocks], case.v_cache[blocks], tables, sub, case.scale,
+                                   True)
+    toks = np.concatenate([np.arange(q0, q0 + lq) for q0, lq, _ in sub])
+    real = np.concatenate([np.arange(q0, q0 + lq) for q0, lq, _ in rows[:case.real_rows]])
+    err_hip = float(np.abs(hip_out.numpy()[toks] - want[toks]).max())
+    err_t32 = float(np.abs(got["t32"].numpy()[toks] - want[toks]).max())
+    diff_all = float((hip_out[real] - got["t32"][real]).abs().max())
+    log(f"[bench] attention numerics: max|GPU - fp64| {err_hip:.2e}, max|CPU fp32 - fp64| {err_t32:.2e} "
+        f"(first 4 rows); max|GPU - CPU fp32| over every row {diff_all:.2e} (bound 2e-2)")
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"the whole batch-64 layer (same inputs as the GPU run, fp32), median of {runs} runs: "
-                      f"{sec * 1e3:.1f} ms/layer", "ms_per_layer": round(sec * 1e3, 2)}
+                      f"{sec * 1e3:.1f} ms/layer", "ms_per_layer": round(sec * 1e3, 2),
+            "numerics": {"max_abs_err_gpu_vs_fp64": err_hip, "max_abs_err_cpu_fp32_vs_fp64": err_t32,
+                         "rows_vs_fp64": len(sub), "max_abs_diff_gpu_vs_cpu_fp32_all_rows": diff_all,
+                         "bound": 2e-2}}
 
 
 def main():
@@ -612,7 +666,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
 
-    case, ms, nbytes, gbs, flops, token_major = attention_bench(args, dev)
+    case, ms, nbytes, gbs, flops, token_major, hip_out = attention_bench(args, dev)
     extra = {"attention_token_major": token_major, "c2": launch_bound_bench(args, dev),
              "draft_block": draft_block_bench(args, dev),
              "qk_norm_rope_store": qk_rope_bench(args, dev)}
@@ -624,7 +678,7 @@ def main():
         extra["verify_round"] = verify_round_bench(args, dev)
     if args.copy_probe == "on":
         extra["copy_probe"] = copy_probe(args, dev)
-    cpu = cpu_baseline(case) if args.cpu_baseline == "on" else None
+    cpu = cpu_baseline(case, hip_out) if args.cpu_baseline == "on" else None
 
     result = {
         "metric": METRIC,
