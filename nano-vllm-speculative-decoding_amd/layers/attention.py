@@ -6,8 +6,8 @@ Mirrors nanovllm/layers/attention.py:
 and the two flash-attn entry points that forward calls, with the keyword arguments it passes:
   paged_attention_varlen(...)        for flash_attn_varlen_func(..., causal=True, block_table=...) (verify branch)
   paged_attention_with_kvcache(...)  for flash_attn_with_kvcache(q[B, Lq, H, D], ...) (decode / draft-block branch)
-Both run nvs_paged_attention (one HIP launch plus a split combine when a row's keys are split) and
-store_kvcache runs nvs_store_kvcache.
+Both run nvs_paged_attention (one HIP launch; when a row's keys are split, the last split of each unit merges the
+partials inside it) and store_kvcache runs nvs_store_kvcache.
 """
 from __future__ import annotations
 
