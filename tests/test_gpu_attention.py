@@ -91,6 +91,29 @@ def test_sixty_two_splits_of_one_long_row(device):
     check(run_varlen(c, device, max_seqlen_k=32768), c)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_shapes_across_split_plans(device, seed):
+    """Seeded random batches (1-16 rows, 0-8 verify tokens, up to 4,000 keys, GQA groups 1/4/8) under graph-sized
+    max_seqlen_k values that give unsplit, split and maximally split plans: every output against the fp64
+    oracle, and the split merge's counters back at zero afterwards."""
+    import random
+    rng = random.Random(1000 + seed)
+    rows = rng.randint(1, 16)
+    hkv = 8
+    hq = hkv * rng.choice([1, 4, 8])
+    k_lens = [rng.randint(1, 4000) for _ in range(rows)]
+    q_lens = [min(rng.randint(0, 8), lk) for lk in k_lens]
+    q_lens[0] = max(q_lens[0], 1)
+    max_k = rng.choice([max(k_lens), 4096, 16384])
+    log_case(f"attention random shapes seed={seed} rows={rows} heads={hq}/{hkv} max_k={max_k} "
+             f"q={q_lens} k={k_lens}")
+    c = wl.verify_attention_case(q_lens, k_lens, hq, hkv, 128, pad_tokens_to=1, seed_qkv=seed)
+    check(run_varlen(c, device, max_seqlen_k=max_k), c)
+    counters = _lib.persistent_workspace("attention_unit_counters", 4, torch.device(device))
+    torch.cuda.synchronize()
+    assert int(counters.view(torch.int32).abs().sum()) == 0
+
+
 def test_c3_full_size(device):
     log_case("attention c3 b64 varlen ctx 2800-3200")
     c = wl.config_c3()
