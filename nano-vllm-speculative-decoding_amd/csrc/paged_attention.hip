@@ -27,8 +27,9 @@
 //   online softmax in fp32 with exp2 (scale * log2 e folded into one multiply); each lane owns one packed row,
 //   the two halves of a row are merged with one cross-lane exchange
 //   O^T[128 x 32] += V^T[128 x 32 keys] . P^T       8 x v_mfma_f32_32x32x16_bf16; P rounded to bf16 as the B
-//                                                    operand straight from the S accumulators; V^T gathered from
-//                                                    the LDS tile with 16-bit reads
+//                                                    operand straight from the S accumulators; V^T read from the
+//                                                    [key][dim] LDS tile with transposing LDS loads
+//                                                    (ds_read_b64_tr_b16, 2 per MFMA)
 #include "nvs_common.hpp"
 
 #include <cmath>
@@ -39,6 +40,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short tr_v4 __attribute__((ext_vector_type(4)));
+typedef short tr_v8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) tr_v4 tr_lds;   // an LDS address of 4 bf16
 
 constexpr int kHeadDim = 128;
 constexpr int kTileRows = 32;    // packed query rows per tile
@@ -207,6 +211,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
 
     uint16_t* ks = tiles + wave * kWaveElems;   // this wave's K tile
     uint16_t* vs = ks + kTileElems;             // and V tile
+    // V^T operand through gfx950's transposing LDS load (ds_read_b64_tr_b16). Within each 16-lane group, lane i
+    // receives element i % 4 of the 8-byte blocks addressed by lanes 4k + i / 4 (k = 0..3), as element k. Lane
+    // 16g + 4k + q addresses key 4 (g / 2) + k, dims 16 (g % 2) + 4q .. + 3 of a 16-key, 32-dim slice of the
+    // [key][dim] tile, so lane l receives keys 4 (l / 32) + 0..3 of dim l % 32: the A-operand run the P^T
+    // operand's key order needs (two loads per MFMA: keys +0 and +8).
+    __attribute__((address_space(3))) uint16_t* vs_l = (__attribute__((address_space(3))) uint16_t*)vs;
+    const int tr_off = (4 * (lane >> 5) + ((lane >> 2) & 3)) * kRowStride + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     const uint16_t* qrow = qs + nl * kQsStride + 8 * gi;
 
     float m_run = -INFINITY;
@@ -270,20 +281,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
         // keys whose P values it holds in pb[hh], from the [key][dim] tile.
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-            const uint16_t* vcol = vs + 32 * db + nl + 4 * gi * kRowStride;
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-                uint32_t w[4];
-#pragma unroll
-                for (int q2 = 0; q2 < 4; ++q2) {
-                    // pair q2 = keys (16hh + 8a + 4gi + b) with (a, b) = (q2 / 2, 2 (q2 % 2)) and b + 1
-                    const int key = 16 * hh + 8 * (q2 >> 1) + 2 * (q2 & 1);
-                    const uint32_t lo = vcol[key * kRowStride];
-                    const uint32_t hi = vcol[(key + 1) * kRowStride];
-                    w[q2] = lo | (hi << 16);
-                }
-                const u32x4 va = {w[0], w[1], w[2], w[3]};
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va), pb[hh], o[db], 0,
+                const tr_lds* p0 = (const tr_lds*)(vs_l + tr_off + 16 * hh * kRowStride + 32 * db);
+                const tr_lds* p1 = (const tr_lds*)(vs_l + tr_off + (16 * hh + 8) * kRowStride + 32 * db);
+                const tr_v4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<tr_lds*>(p0));
+                const tr_v4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<tr_lds*>(p1));
+                const tr_v8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, v8), pb[hh], o[db], 0,
                                                                 0, 0);
             }
         }
