@@ -108,7 +108,8 @@ def _paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     # a plan that splits keys merges them in the launch: per-unit counters, zero between calls
     counters = None
     if nbytes.value > 0:
-        units = num_rows * Hkv * -(-(H // Hkv) * max_seqlen_q // 32)
+        q_tiles = ((H // Hkv) * max_seqlen_q + 31) // 32     # 32 packed query rows per tile
+        units = num_rows * Hkv * q_tiles
         counters = _lib.persistent_workspace("attention_unit_counters", 4 * max(units, _MIN_COUNTER_UNITS), q.device)
     _lib.check(lib.nvs_paged_attention(
         q.data_ptr(), q.stride(0), q.stride(1), T, k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
