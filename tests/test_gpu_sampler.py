@@ -242,6 +242,42 @@ def test_fused_accept_is_bit_exact(device, name, kwargs):
     print(f"{name}: accepted {n_got.float().mean():.2f} of {case.drafts.shape[1]} on average")
 
 
+def random_sampler_config(seed):
+    """A seeded random verify batch: rows, drafts, vocabulary (aligned or not), fixed or variable lengths, logit
+    scale and dtype, and per-row top-k (0 = off, mixed with truncating rows), top-p and temperature."""
+    import random
+    rng = random.Random(2000 + seed)
+    batch = rng.randint(1, 24)
+    k = rng.randint(1, 8)
+    vocab = rng.choice([rng.randint(500, 70000), 4 * rng.randint(250, 40000)])
+    varlen = rng.random() < 0.5
+    all_dense = rng.random() < 0.2
+    top_k = [0 if all_dense else rng.choice([0, 1, 5, 20, 64, 64, 200]) for _ in range(batch)]
+    if not all_dense and max(top_k) == 0:
+        top_k[0] = 64
+    kwargs = dict(batch=batch, num_drafts=k, vocab=vocab, top_k=top_k,
+                  top_p=[rng.choice([1.0, 1.0, 0.9, 0.5]) for _ in range(batch)],
+                  temperature=[rng.choice([1.0, 1.0, 0.7, 1.3]) for _ in range(batch)],
+                  sigma=rng.choice([1.0, 3.0, 8.0]),
+                  logits_dtype=rng.choice([torch.float32, torch.bfloat16]))
+    if varlen:
+        kwargs["verified_lens"] = [rng.randint(1, k + 1) for _ in range(batch)]
+    return kwargs
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_fused_accept_random_configs_are_bit_exact(device, seed):
+    """Seeded random batches through the one-launch accept (and, when no row truncates, the dense race after it):
+    accepted lengths and tail tokens bit for bit equal to the oracle's, given the same uniforms and noise."""
+    kwargs = random_sampler_config(seed)
+    log_case(f"fused accept random config seed={seed}: {kwargs}")
+    case = wl.sampler_case(draft_probs_fn=draft_probs, **kwargs)
+    n_got, tail_got = run_fused(case, device)
+    n_want, tail_want = run_oracle(case)
+    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want)
+    assert torch.equal(tail_got, tail_want)
+
+
 def ordered_logits(case, kind):
     """Target logits laid out against the streaming pass's first bound (taken from the first two 8192-element
     batches of a row): ascending rows put every large value after it (the lists fill and the row takes the exact
