@@ -170,11 +170,11 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 }
 
 // Inclusive prefix sum over the wave.
-__device__ __forceinline__ float wave_scan_incl(float v) {
+__device__ __forceinline__ double wave_scan_incl_f64(double v) {
     const int l = lane_id();
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const float w = __shfl_up(v, o);
+        const double w = __shfl_up(v, o);
         if (l >= o) v += w;
     }
     return v;
@@ -568,24 +568,27 @@ __device__ float top_p_threshold(SelShared& sh, int rank, int K, float top_p, fl
             lsum += e[i];
         }
         const float total = wave_sum(lsum);
-        // local cumsum of nucleus values, then the lanes' exclusive prefix
-        float loc = 0.f;
+        // The nucleus cumsum as torch's CPU cumsum of fp32 computes it: accumulated in double, each prefix rounded
+        // to float, then the float subtraction of the entry (spec_sampler.py:91). An fp32 running sum reaches 1.0
+        // early on a peaked row and would cut entries the reference keeps. Local sums first, then the lanes'
+        // exclusive prefix.
+        double loc = 0.0;
         for (int i = 0; i < per && i < 16; ++i) {
             e[i] = e[i] / total;
-            loc += e[i];
+            loc += static_cast<double>(e[i]);
         }
-        const float incl = wave_scan_incl(loc);
-        float run = incl - loc;
+        const double incl = wave_scan_incl_f64(loc);
+        double run = incl - loc;
         int kept = 0;
         for (int i = 0; i < per && i < 16; ++i) {
             const int r = l * per + i;
             if (r < rank) {
-                run += e[i];
-                const float before = run - e[i];
+                run += static_cast<double>(e[i]);
+                const float before = static_cast<float>(run) - e[i];
                 kept += (before < top_p) ? 1 : 0;
             }
         }
-        float last_cum = __shfl(incl, 63);  // cumsum at rank - 1 (all later entries add zero)
+        const float last_cum = static_cast<float>(__shfl(incl, 63));  // cumsum at rank - 1 (later entries add 0)
         int kept_all = static_cast<int>(wave_sum(static_cast<float>(kept)));
         if (last_cum < top_p) kept_all += K - rank;
         if (l == 0) {
@@ -607,7 +610,8 @@ __device__ float wave_top_p_threshold64(uint32_t key_l, int rank, int K, float t
     const float e = (l < rank) ? expf(nvs::key_float(key_l) - m) : 0.f;
     const float total = wave_sum(e);
     const float nucleus = e / total;
-    const float cum = wave_scan_incl(nucleus);
+    // the cumsum accumulated in double and rounded per prefix, as torch's CPU cumsum of fp32 (see top_p_threshold)
+    const float cum = static_cast<float>(wave_scan_incl_f64(static_cast<double>(nucleus)));
     const float before = cum - nucleus;
     int kept_all = __popcll(__ballot(l < rank && before < top_p));
     const float last_cum = __shfl(cum, 63);   // cumsum at rank - 1 (all later entries add zero)

@@ -278,6 +278,68 @@ def test_fused_accept_random_configs_are_bit_exact(device, seed):
     assert torch.equal(tail_got, tail_want)
 
 
+def nucleus_margin(scaled_row, top_k, top_p, max_top_k):
+    """How far the reference's nucleus test on one row is from a tie: the smallest |mass_before - top_p| over the
+    row's top-k candidates and the total mass (spec_sampler.py:87-93). A kept set may legitimately differ from the
+    oracle's only when this is a few ulps: the comparison then turns on the last bits of the fp32 softmax, which
+    the GPU's exp and sum round differently from torch's CPU kernel."""
+    K = min(max_top_k, scaled_row.numel())
+    cand = scaled_row.topk(K).values.clone()
+    cand[max(top_k, 1):] = float("-inf")
+    nucleus = torch.softmax(cand, dim=-1)
+    cum = nucleus.cumsum(dim=-1)
+    before = (cum - nucleus)[:max(top_k, 1)]
+    return float(torch.cat([before, cum[-1:]]).sub(top_p).abs().min())
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_unfused_rows_on_random_configs(device, seed):
+    """The same seeded random batches through the unfused entry points, each against the oracle:
+    probs_from_logits (per-token parameters, values within 1e-5 relative and the same kept set), truncate_logits
+    (bit for bit), the race of sample() and accept_random over the oracle's own p (bit for bit).
+    Kept sets are compared on probabilities at or above the smallest normal fp32 (1.18e-38): an untruncated row
+    with a wide logit range has entries the CPU softmax keeps as denormals and the GPU's exp flushes to zero;
+    every such disagreement must lie below that bound on both sides. A top-p row whose nucleus test is within
+    4 ulps of a tie (nucleus_margin) may cut elsewhere; any other difference fails."""
+    kwargs = random_sampler_config(seed)
+    log_case(f"unfused sampler rows random config seed={seed}")
+    case = wl.sampler_case(draft_probs_fn=draft_probs, **kwargs)
+    logits = case.logits.float()
+    B, k = case.drafts.shape
+    lens = case.verified_lens if case.verified_lens is not None else torch.full((B,), k + 1, dtype=torch.int64)
+    t, tk, tp = (x.repeat_interleave(lens) for x in (case.temperatures, case.top_k, case.top_p))
+    st = ns.SamplingTensors(t.to(device), tk.to(device), tp.to(device), case.max_top_k, case.has_top_p,
+                            bool((tk > 0).all()))
+    want = ref.probs_from_logits(logits, t, tk, tp, case.max_top_k, case.has_top_p)
+    got = ns.probs_from_logits(logits.to(device), st).cpu()
+    scaled = logits / t[:, None]
+    trunc_got = ns.truncate_logits(scaled.to(device), st).cpu()
+    trunc_want = ref.truncate_logits(scaled, tk, tp, case.max_top_k, case.has_top_p)
+    normal = torch.finfo(torch.float32).tiny
+    ties = []
+    for r in range(logits.shape[0]):
+        same = (torch.equal(got[r] >= normal, want[r] >= normal) and
+                torch.equal(torch.isfinite(trunc_got[r]), torch.isfinite(trunc_want[r])))
+        if not same:
+            margin = nucleus_margin(scaled[r], int(tk[r]), float(tp[r]), case.max_top_k)
+            assert case.has_top_p and int(tk[r]) > 0 and margin <= 4 * 2.0 ** -23, \
+                f"position {r}: kept sets differ with nucleus margin {margin:.3e}"
+            ties.append((r, margin))
+            continue
+        differ = (got[r] > 0) != (want[r] > 0)
+        assert bool((got[r][differ] < normal).all() and (want[r][differ] < normal).all())
+        torch.testing.assert_close(got[r], want[r], rtol=1e-5, atol=1e-7)
+        assert torch.equal(trunc_got[r], trunc_want[r])
+    if ties:
+        print(f"seed {seed}: nucleus ties (position, margin): {ties}")
+    w = want[torch.cumsum(lens, 0) - 1]                      # each row's bonus position
+    assert torch.equal(ns.race(w.to(device), case.noise.to(device)).cpu(), ref.race(w, case.noise))
+    n_want, tail_want = ref.accept_random_varlen(want, case.q, case.drafts, lens, case.uniforms, case.noise)
+    n_got, tail_got = ns.accept_random_with_draws(want.to(device), case.q.to(device), case.drafts.to(device),
+                                                  lens.to(device), case.uniforms.to(device), case.noise.to(device))
+    assert torch.equal(n_got.cpu(), n_want) and torch.equal(tail_got.cpu(), tail_want)
+
+
 def ordered_logits(case, kind):
     """Target logits laid out against the streaming pass's first bound (taken from the first two 8192-element
     batches of a row): ascending rows put every large value after it (the lists fill and the row takes the exact
