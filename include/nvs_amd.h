@@ -153,7 +153,8 @@ int nvs_paged_attention(const void* q, int64_t q_token_stride, int64_t q_head_st
  *   top_p f32 (1 = off); max_top_k and has_top_p are the host flags of SamplingTensors.
  *   Truncation = truncate_logits (spec_sampler.py:72-96): keep s >= threshold, ties kept, HuggingFace order
  *   temperature -> top-k -> top-p-within-top-k; probabilities = softmax over the kept set.
- * max_top_k above 1024 is NVS_ERR_UNSUPPORTED. */
+ * Any max_top_k >= 0 (top_k up to the vocabulary, sampling_params.py:15-16); windows wider than 1024 values take a
+ * slower exact path over the row. nvs_markov_draw alone is limited to max_top_k <= 1024 (NVS_ERR_UNSUPPORTED). */
 
 /* probs_from_logits (spec_sampler.py:65-69): dense fp32 probabilities [n_pos, V] into probs (row stride V). */
 int nvs_probs_from_logits_workspace_size(int64_t n_pos, int64_t vocab, int max_top_k, size_t* bytes);

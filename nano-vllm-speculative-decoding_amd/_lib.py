@@ -141,19 +141,25 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
 
 
 _persistent: dict = {}
+# Buffers replaced by a larger one stay referenced until the process ends: a graph captured while one of them was
+# current keeps its address in its kernel arguments, and every call leaves the buffer zero, so such a graph still
+# replays correctly after a later, larger eager call grew the buffer.
+_superseded: list = []
 
 
 def persistent_workspace(name: str, nbytes: int, device: torch.device) -> torch.Tensor:
     """A zero-initialised device buffer kept across calls, for kernels that keep counters in it and leave them at
     zero when they finish (the row and unit counters of the one-launch accept, race and split-key attention). One
     buffer per (name, device); calls that share it must be ordered on one stream. It is created outside graph
-    capture: warm up once eagerly before capturing."""
+    capture: warm up once eagerly before capturing. A buffer that is outgrown is replaced but never freed."""
     key = (name, device.type, device.index)
     buf = _persistent.get(key)
     if buf is None or buf.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError(f"nvs_amd: the {name} workspace must be created before graph capture; "
                                "run the op once eagerly first")
+        if buf is not None:
+            _superseded.append(buf)
         buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
         _persistent[key] = buf
     return buf

@@ -22,7 +22,7 @@
 //   load    K and V rows of the chunk with coalesced streaming 16-byte loads (4 keys x 256 B per instruction,
 //           page and block id clamped into range) and stage them into the wave's padded LDS tiles; the loads of
 //           chunk c + 4 (the wave's next chunk) are issued right after, so they are in flight during the math
-//   S^T[32 keys x 32 rows] = K[32 x 128] . Q^T      8 x v_mfma_f32_32x32x16_bf16, K read from the LDS tile in the
+//   S^T[32 keys x 32 rows] = K[32 x 128] . Q^T      8 x v_mfma_f32_32x32x16_bf16 (_f16 for fp16 caches), K read from the LDS tile in the
 //                                                    A-operand layout, Q from the LDS query tile
 //   online softmax in fp32 with exp2 (scale * log2 e folded into one multiply); each lane owns one packed row,
 //   the two halves of a row are merged with one cross-lane exchange
@@ -37,12 +37,34 @@
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short tr_v4 __attribute__((ext_vector_type(4)));
 typedef short tr_v8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) tr_v4 tr_lds;   // an LDS address of 4 bf16
+
+// The two 16-bit element types the kernel serves (bf16, and fp16 for models built in half precision,
+// model_runner.py:55-57): element, 8-element MFMA operand, the 32x32x16 MFMA and the fp32 -> 16-bit rounding
+// (round to nearest even).
+template <int DT> struct Elem16;
+template <> struct Elem16<NVS_DTYPE_BF16> {
+    typedef __bf16 type;
+    typedef bf16x8 vec8;
+    static __device__ __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t bits(float f) { return nvs::float_to_bf16_bits(f); }
+};
+template <> struct Elem16<NVS_DTYPE_F16> {
+    typedef _Float16 type;
+    typedef f16x8 vec8;
+    static __device__ __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t bits(float f) { return __half_as_ushort(__float2half(f)); }
+};
 
 constexpr int kHeadDim = 128;
 constexpr int kTileRows = 32;    // packed query rows per tile
@@ -126,7 +148,10 @@ __device__ __forceinline__ int active_splits(int lk, int split_len) {
 
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
+template <int DT>
 __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
+    using E = Elem16<DT>;
+    using V8 = typename E::vec8;
     __shared__ __attribute__((aligned(16))) uint16_t tiles[kWaves * kWaveElems];
     __shared__ __attribute__((aligned(16))) uint16_t qs[kTileRows * kQsStride];
     __shared__ float sm_m[kWaves][kTileRows];
@@ -248,10 +273,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
         f32x16 acc = f32x16{};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const bf16x8 kb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ks + nl * kRowStride +
-                                                                                          16 * i + 8 * gi));
-            const bf16x8 qb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qrow + 16 * i));
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qb, acc, 0, 0, 0);
+            const V8 kb = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(ks + nl * kRowStride + 16 * i +
+                                                                                  8 * gi));
+            const V8 qb = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(qrow + 16 * i));
+            acc = E::mfma(kb, qb, acc);
         }
         float mx = -INFINITY;
 #pragma unroll
@@ -265,12 +290,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
         const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
         float ps = 0.f;
-        bf16x8 pb[2];
+        V8 pb[2];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const float pj = __builtin_amdgcn_exp2f(acc[j] - m_use);
             ps += pj;
-            pb[j >> 3][j & 7] = static_cast<__bf16>(pj);
+            pb[j >> 3][j & 7] = static_cast<typename E::type>(pj);
         }
         l_run = l_run * alpha + ps;
         m_run = m_new;
@@ -288,8 +313,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
                 const tr_v4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<tr_lds*>(p0));
                 const tr_v4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<tr_lds*>(p1));
                 const tr_v8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, v8), pb[hh], o[db], 0,
-                                                                0, 0);
+                o[db] = E::mfma(__builtin_bit_cast(V8, v8), pb[hh], o[db]);
             }
         }
     };
@@ -348,10 +372,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
             for (int jq = 0; jq < 4; ++jq) {
                 const int d = 32 * db + 8 * jq + 4 * gi;
-                const uint32_t lo = nvs::float_to_bf16_bits(o[db][4 * jq + 0] * inv) |
-                                    (static_cast<uint32_t>(nvs::float_to_bf16_bits(o[db][4 * jq + 1] * inv)) << 16);
-                const uint32_t hi = nvs::float_to_bf16_bits(o[db][4 * jq + 2] * inv) |
-                                    (static_cast<uint32_t>(nvs::float_to_bf16_bits(o[db][4 * jq + 3] * inv)) << 16);
+                const uint32_t lo = E::bits(o[db][4 * jq + 0] * inv) | (E::bits(o[db][4 * jq + 1] * inv) << 16);
+                const uint32_t hi = E::bits(o[db][4 * jq + 2] * inv) | (E::bits(o[db][4 * jq + 3] * inv) << 16);
                 *reinterpret_cast<u32x2*>(op + d) = u32x2{lo, hi};
             }
         }
@@ -460,8 +482,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
         if (qpm >= ri.lq || ri.q0 + qpm >= a.n_tokens || ri.q0 + qpm < 0) continue;
         const int hm = g * a.group + (nm - qpm * a.group);
         const float inv = inv_l[row];
-        const uint32_t bits = nvs::float_to_bf16_bits(acc[k][0] * inv) |
-                              (static_cast<uint32_t>(nvs::float_to_bf16_bits(acc[k][1] * inv)) << 16);
+        const uint32_t bits = E::bits(acc[k][0] * inv) | (E::bits(acc[k][1] * inv) << 16);
         *reinterpret_cast<uint32_t*>(a.out + static_cast<int64_t>(ri.q0 + qpm) * a.o_ts +
                                      static_cast<int64_t>(hm) * a.o_hs + 2 * (tid & 63)) = bits;
     }
@@ -541,8 +562,8 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_token_stride, int64_
     nvs::clear_error();
     int st = validate_sizes(n_rows, n_heads, n_kv_heads, head_dim, max_seqlen_q, max_seqlen_k);
     if (st != NVS_OK) return st;
-    NVS_CHECK(dtype == NVS_DTYPE_BF16, NVS_ERR_UNSUPPORTED, "paged_attention: dtype %d unsupported (only bf16)",
-              dtype);
+    NVS_CHECK(dtype == NVS_DTYPE_BF16 || dtype == NVS_DTYPE_F16, NVS_ERR_UNSUPPORTED,
+              "paged_attention: dtype %d unsupported (bf16 or fp16)", dtype);
     const bool varlen = cu_seqlens_q != nullptr || cu_seqlens_k != nullptr;
     NVS_CHECK(!varlen || (cu_seqlens_q != nullptr && cu_seqlens_k != nullptr), NVS_ERR_INVALID,
               "paged_attention: cu_seqlens_q and cu_seqlens_k must both be given (varlen) or both NULL");
@@ -619,6 +640,10 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_token_stride, int64_
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(n_kv_heads * plan.q_tiles, n_rows, plan.n_splits);
-    hipLaunchKernelGGL(attn_split_kernel, grid, dim3(kThreads), 0, s, a);
+    if (dtype == NVS_DTYPE_BF16) {
+        hipLaunchKernelGGL(attn_split_kernel<NVS_DTYPE_BF16>, grid, dim3(kThreads), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(attn_split_kernel<NVS_DTYPE_F16>, grid, dim3(kThreads), 0, s, a);
+    }
     return nvs::check_launch("paged_attention split kernel");
 }

@@ -21,6 +21,7 @@
 // q and E only at the kept indices. A finalize kernel per batch row counts the accepted prefix and picks the race
 // of the position that follows it (or races over the whole vocabulary for rows that do not truncate).
 #include "nvs_common.hpp"
+#include "spec_accept.hpp"
 
 #include <cmath>
 
@@ -626,10 +627,159 @@ struct RowStats {
     bool dense;   // kept set not held in the candidate list
 };
 
+// ---------------------------------------------------------------- windows wider than the candidate lists
+// A row whose top-k window holds more than kMaxTopK values (top_k up to the vocabulary, sampling_params.py:15-16)
+// keeps nothing in LDS: the rank-th largest value comes from a radix select over the row, the top-p threshold from
+// a radix descent over nucleus mass (below), and the softmax sum and every later use re-read the row.
+
+// Nucleus probabilities (in [0, 1]) are summed in 64-bit fixed point with 62 fraction bits: integer sums are exact
+// whatever order the atomics land in, so the descent is deterministic; a probability below 2^-62 adds nothing.
+constexpr double kMassScale = 4611686018427387904.0;   // 2^62
+
+__device__ __forceinline__ unsigned long long mass_fixed(float n) {
+    return static_cast<unsigned long long>(static_cast<double>(n) * kMassScale);
+}
+
+// Whether top-p keeps the first rank holding a value of nucleus probability n, when the ranks before it hold
+// nucleus mass `before` (fixed point): mass_before = cumsum - nucleus (spec_sampler.py:90-91), the cumsum as torch's
+// CPU cumsum of fp32 forms it (a double running sum rounded to float at each prefix), tested < top_p.
+__device__ __forceinline__ bool nucleus_keeps(unsigned long long before, float n, float top_p) {
+    const double cum = static_cast<double>(before) / kMassScale + static_cast<double>(n);
+    return static_cast<float>(cum) - n < top_p;
+}
+
+// Top-p threshold of a wide window without sorting it. The nucleus is the softmax over the window's `rank` values:
+// the n_gt values above thr plus rank - n_gt copies of thr (the window's ranks past top_k are -inf,
+// spec_sampler.py:82-89), and kept = #(ranks whose mass_before < top_p); the threshold is the kept-th largest.
+// mass_before grows with the rank, so that is the smallest window value whose first rank is kept. A radix descent
+// over the window's keys finds it: per 8-bit digit, each bin's nucleus mass, key count and largest key; the bin
+// whose largest key is kept and that lies lowest holds it, and the mass of the bins above carries into the next
+// digit. Returns thr when no rank is kept (top_p <= 0).
+template <class ForEach>
+__device__ float wide_top_p_threshold(ForEach for_each, uint32_t thr_key, uint32_t n_gt, int rank, float m,
+                                      float top_p, SelShared& sh) {
+    const float thr = nvs::key_float(thr_key);
+    const uint32_t copies = static_cast<uint32_t>(rank) - n_gt;
+    float tot = 0.f;
+    for_each([&](uint32_t key) {
+        if (key > thr_key) tot += expf(nvs::key_float(key) - m);
+    });
+    tot = block_sum(tot, sh) + static_cast<float>(copies) * expf(thr - m);
+    // the refinement histograms' space is free on this path: masses, then largest keys; counts in sh.hist
+    unsigned long long* hmass = reinterpret_cast<unsigned long long*>(&sh.whist[0][0]);
+    uint32_t* hmax = &sh.whist[4][0];
+    uint32_t* hcnt = sh.hist;
+    __shared__ unsigned long long desc_above;
+    __shared__ uint32_t desc_digit;
+    __shared__ int desc_found;
+    uint32_t prefix = 0u, mask = 0u;
+    unsigned long long above = 0ull;   // nucleus mass of the window's keys above the current digit's range
+#pragma unroll 1
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+            hmass[i] = 0ull;
+            hmax[i] = 0u;
+            hcnt[i] = 0u;
+        }
+        __syncthreads();
+        for_each([&](uint32_t key) {
+            if (key <= thr_key || (key & mask) != prefix) return;   // thr's copies are counted below
+            const uint32_t bin = (key >> shift) & 255u;
+            atomicAdd(&hmass[bin], mass_fixed(expf(nvs::key_float(key) - m) / tot));
+            atomicAdd(&hcnt[bin], 1u);
+            atomicMax(&hmax[bin], key);
+        });
+        if (threadIdx.x == 0 && (thr_key & mask) == prefix && copies > 0u) {
+            const uint32_t bin = (thr_key >> shift) & 255u;
+            atomicAdd(&hmass[bin], static_cast<unsigned long long>(copies) * mass_fixed(expf(thr - m) / tot));
+            atomicAdd(&hcnt[bin], copies);
+            atomicMax(&hmax[bin], thr_key);
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            // lane l holds bins 4l .. 4l+3; the bins of higher lanes lie above them
+            const int l = lane_id();
+            unsigned long long mb[4];
+            uint32_t cb[4], kb[4];
+            unsigned long long lane_mass = 0ull;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                mb[i] = hmass[4 * l + i];
+                cb[i] = hcnt[4 * l + i];
+                kb[i] = hmax[4 * l + i];
+                lane_mass += mb[i];
+            }
+            const int64_t incl = wave_scan_incl_i64(static_cast<int64_t>(lane_mass));
+            const int64_t total = __shfl(incl, 63);
+            unsigned long long run = above + static_cast<unsigned long long>(total - incl);
+            uint32_t lowest = 256u;
+            unsigned long long lowest_above = 0ull;
+#pragma unroll
+            for (int i = 3; i >= 0; --i) {
+                if (cb[i] > 0u && nucleus_keeps(run, expf(nvs::key_float(kb[i]) - m) / tot, top_p)) {
+                    lowest = static_cast<uint32_t>(4 * l + i);
+                    lowest_above = run;
+                }
+                run += mb[i];
+            }
+            const uint32_t best = 256u - wave_max_u32(256u - lowest);
+            if (best < 256u && lowest == best) {
+                desc_above = lowest_above;
+                desc_digit = best;
+            }
+            if (l == 0) desc_found = best < 256u ? 1 : 0;
+        }
+        __syncthreads();
+        if (!desc_found) return thr;
+        above = desc_above;
+        prefix |= desc_digit << shift;
+        mask |= 255u << shift;
+        __syncthreads();   // every thread has read the digit before the next pass rewrites it
+    }
+    return nvs::key_float(prefix);
+}
+
+// Row statistics of a wide window: the rank-th largest value by a radix select over the row, the row maximum, the
+// top-p threshold as above, and the softmax sum over the kept values; the kept set stays in the row (dense).
+template <int DT, bool VEC>
+__device__ RowStats wide_row_stats(const SelArgs& a, const void* row, float temp, bool unit_temp, int rank,
+                                   float top_p, SelShared& sh) {
+    auto for_each = [&](auto&& fn) {
+        for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
+            float v[kVpt];
+            load_vals<DT, VEC>(row, e0, a.vocab, v);
+#pragma unroll
+            for (int vi = 0; vi < kVpt; ++vi) {
+                const uint32_t key = sel_key(scale_logit(v[vi], temp, unit_temp));
+                if (key != 0u) fn(key);
+            }
+        }
+    };
+    uint32_t n_gt = 0, n_eq = 0;
+    const uint32_t thr_key = radix_select(for_each, static_cast<uint32_t>(rank), sh, &n_gt, &n_eq);
+    uint32_t mk = 0u;
+    for_each([&](uint32_t key) { mk = max(mk, key); });
+    mk = block_max_u32(mk, sh);
+    RowStats rs;
+    rs.m = nvs::key_float(mk);
+    rs.theta = nvs::key_float(thr_key);
+    if (a.has_top_p) rs.theta = wide_top_p_threshold(for_each, thr_key, n_gt, rank, rs.m, top_p, sh);
+    const uint32_t theta_key = nvs::float_key(rs.theta);
+    float z = 0.f;
+    for_each([&](uint32_t key) {
+        if (key >= theta_key) z += expf(nvs::key_float(key) - rs.m);
+    });
+    rs.z = block_sum(z, sh);
+    rs.dense = true;
+    return rs;
+}
+
 // Full-row exact path (candidate list overflowed): radix select on the row, then rebuild the candidate list.
 template <int DT, bool VEC>
 __device__ RowStats exact_row_stats(const SelArgs& a, const void* row, float temp, bool unit_temp,
                                     int rank, int K, float top_p, SelShared& sh) {
+    if (rank > kMaxTopK) return wide_row_stats<DT, VEC>(a, row, temp, unit_temp, rank, top_p, sh);
     auto for_each = [&](auto&& fn) {
         for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
             float v[kVpt];
@@ -706,119 +856,6 @@ __device__ RowStats exact_row_stats(const SelArgs& a, const void* row, float tem
     }
     rs.z = block_sum(z, sh);
     return rs;
-}
-
-// Finish batch row b of the fused accept (run by the workgroup whose position arrived last): the accepted prefix
-// n from the positions' decisions, then the tail = the race of position start + n, which that position already ran
-// over its kept set, or, for a row that does not truncate, a race over the whole vocabulary run here. The caller
-// has acquired the other positions' records (count_position).
-template <int DT>
-__device__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L, SelShared& sh) {
-    const int kd = a.k;
-    if (threadIdx.x < 64) {
-        // wave 0: lane i loads the record of position start + c0 + i, all in one round trip; the first position
-        // that is rejected or cannot be accepted ends the prefix and its record gives the tail
-        const int lane = threadIdx.x;
-        const int64_t lim = min(min(L - 1, static_cast<int64_t>(kd)), a.n_pos - start);   // n stays <= lim
-        for (int64_t c0 = 0;; c0 += 64) {
-            const int64_t pos = min(start + c0 + lane, a.n_pos - 1);
-            const PosRecord r = load_record(a.rec + pos);
-            const bool stop = (c0 + lane >= lim) || !r.acc;
-            const uint64_t bal = __ballot(stop);
-            if (bal == 0ull) continue;   // all 64 accepted: the next 64
-            const int first = __ffsll(static_cast<long long>(bal)) - 1;
-            if (lane == first) {
-                const int64_t n = c0 + first;
-                sh.fin_n = n;
-                sh.fin_rec = r;
-                if (!(r.flags & kFlagDense)) {   // the tail is that position's own race: the row is done
-                    a.n_accept[b] = n;
-                    a.tail[b] = r.race;
-                    a.counters[b] = 0;   // ready for the next call
-                    if (a.dense_race != nullptr) a.dense_race[b].valid = 0;
-                } else if (a.dense_race != nullptr) {
-                    // the race over the whole vocabulary runs in the dense race kernels, spread over the chip
-                    DenseRace d;
-                    d.pos = min(start + n, a.n_pos - 1);
-                    d.qrow = (n == L - 1) ? -1 : b * kd + (n < kd - 1 ? n : kd - 1);
-                    d.m = r.m;
-                    d.z = r.z;
-                    d.temp = r.temp;
-                    d.valid = 1;
-                    a.dense_race[b] = d;
-                    a.n_accept[b] = n;
-                    a.counters[b] = 0;
-                }
-            }
-            break;
-        }
-    }
-    __syncthreads();
-    const int64_t n = sh.fin_n;
-    const PosRecord r = sh.fin_rec;
-    if ((r.flags & kFlagDense) && a.dense_race == nullptr) {
-        const int64_t pos = min(start + n, a.n_pos - 1);
-        const bool bonus = (n == L - 1);
-        const int64_t qn = n < kd - 1 ? n : kd - 1;
-        const float* qrow = a.q + (b * kd + qn) * a.vocab;
-        const float* erow = a.noise + b * a.vocab;
-        const char* row = static_cast<const char*>(a.logits) + pos * a.row_stride * nvs::dtype_size(DT);
-        const uint32_t theta_key = r.theta == -INFINITY ? 0u : nvs::float_key(r.theta);
-        const float mu = (r.m == -INFINITY) ? 0.f : r.m;
-        const bool unit_temp = (r.temp == 1.f);
-        uint64_t best = 0;
-        for (int64_t i = threadIdx.x; i < a.vocab; i += blockDim.x) {
-            const float sc = scale_logit(nvs::load_as_float<DT>(row, i), r.temp, unit_temp);
-            const float p = (sel_key(sc) >= theta_key && sc == sc) ? expf(sc - mu) / r.z : 0.f;
-            const float w = bonus ? p : fmaxf(p - qrow[i], 0.f);
-            const float score = w / erow[i];
-            const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
-                                 static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
-            best = best > k64 ? best : k64;
-        }
-        best = block_max_u64(best, sh);
-        if (threadIdx.x == 0) {
-            a.n_accept[b] = n;
-            a.tail[b] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
-            a.counters[b] = 0;  // ready for the next call
-        }
-    }
-}
-
-// Count a finished position of batch row b on the row's counter; the position that counts last finishes the row.
-// Returns whether this position counted last. The caller stored its record with store_record: the wait below
-// holds the add back until those stores are performed at the coherence point, and the finishing workgroup issues
-// its record loads (load_record, also at the coherence point) only after its own add has returned, so it reads
-// every record of the row.
-__device__ __forceinline__ bool count_position(int* counter, int64_t n_positions) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): every store of this wave has completed
-    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return before == static_cast<int>(n_positions) - 1;
-}
-
-// The end of one vocabulary chunk of a race spread over (row, chunk) workgroups, run by wave 0 of the chunk's
-// workgroup: lane 0 publishes the chunk's best key to the row's partials at the coherence point and counts the
-// chunk on the row's counter (count_position); the workgroup that counts last reads every chunk's key of the row
-// (one load per lane, at the coherence point), resets the counter for the next call and returns true with the
-// row's best key in winner. Every lane of wave 0 must call it; the result is uniform over the wave.
-__device__ __forceinline__ bool finish_race_chunk(uint64_t* row_partials, int n_chunks, int c, uint64_t key,
-                                                  int* counter, uint64_t& winner) {
-    const int lane = threadIdx.x & 63;
-    int last = 0;
-    if (lane == 0) {
-        __hip_atomic_store(row_partials + c, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = count_position(counter, n_chunks) ? 1 : 0;
-    }
-    last = __builtin_amdgcn_readfirstlane(last);
-    if (!last) return false;
-    uint64_t best = 0;
-    for (int j = lane; j < n_chunks; j += 64) {
-        const uint64_t v = __hip_atomic_load(row_partials + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        best = best > v ? best : v;
-    }
-    winner = wave_max_u64(best);
-    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return true;
 }
 
 // ---------------------------------------------------------------- q as candidate rows
@@ -963,6 +1000,135 @@ __device__ float q_hash_lookup(SelShared& sh, int64_t token) {
         h = (h + 1u) & (kQHash - 1);
     }
     return 0.f;
+}
+
+// Finish batch row b of the fused accept (run by the workgroup whose position arrived last): the accepted prefix
+// n from the positions' decisions, then the tail = the race of position start + n, which that position already ran
+// over its kept set, or, for a row that does not truncate, a race over the whole vocabulary run here. The caller
+// has acquired the other positions' records (count_position).
+template <int DT>
+__device__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L, SelShared& sh) {
+    const int kd = a.k;
+    if (threadIdx.x < 64) {
+        // wave 0: lane i loads the record of position start + c0 + i, all in one round trip; the first position
+        // that is rejected or cannot be accepted ends the prefix and its record gives the tail
+        const int lane = threadIdx.x;
+        const int64_t lim = min(min(L - 1, static_cast<int64_t>(kd)), a.n_pos - start);   // n stays <= lim
+        for (int64_t c0 = 0;; c0 += 64) {
+            const int64_t pos = min(start + c0 + lane, a.n_pos - 1);
+            const PosRecord r = load_record(a.rec + pos);
+            const bool stop = (c0 + lane >= lim) || !r.acc;
+            const uint64_t bal = __ballot(stop);
+            if (bal == 0ull) continue;   // all 64 accepted: the next 64
+            const int first = __ffsll(static_cast<long long>(bal)) - 1;
+            if (lane == first) {
+                const int64_t n = c0 + first;
+                sh.fin_n = n;
+                sh.fin_rec = r;
+                if (!(r.flags & kFlagDense)) {   // the tail is that position's own race: the row is done
+                    a.n_accept[b] = n;
+                    a.tail[b] = r.race;
+                    a.counters[b] = 0;   // ready for the next call
+                    if (a.dense_race != nullptr) a.dense_race[b].valid = 0;
+                } else if (a.dense_race != nullptr) {
+                    // the race over the whole vocabulary runs in the dense race kernels, spread over the chip
+                    DenseRace d;
+                    d.pos = min(start + n, a.n_pos - 1);
+                    d.qrow = (n == L - 1) ? -1 : b * kd + (n < kd - 1 ? n : kd - 1);
+                    d.m = r.m;
+                    d.z = r.z;
+                    d.temp = r.temp;
+                    d.valid = 1;
+                    a.dense_race[b] = d;
+                    a.n_accept[b] = n;
+                    a.counters[b] = 0;
+                }
+            }
+            break;
+        }
+    }
+    __syncthreads();
+    const int64_t n = sh.fin_n;
+    const PosRecord r = sh.fin_rec;
+    if ((r.flags & kFlagDense) && a.dense_race == nullptr) {
+        const int64_t pos = min(start + n, a.n_pos - 1);
+        const bool bonus = (n == L - 1);
+        const int64_t qn = n < kd - 1 ? n : kd - 1;
+        const int64_t qslot = b * kd + qn;
+        // q of the rejected draft: the dense row, or its candidate rows (hashed in LDS when they fit)
+        const bool sparse = a.q_ids != nullptr;
+        const bool hashed = sparse && !bonus && a.q_cand <= kQHash / 2;
+        if (hashed) build_q_hash(a, qslot, sh);
+        auto q_at = [&](int64_t i) -> float {
+            if (!sparse) return a.q[qslot * a.vocab + i];
+            return hashed ? q_hash_lookup(sh, i) : sparse_q_scan(a, qslot, i);
+        };
+        const float* erow = a.noise + b * a.vocab;
+        const char* row = static_cast<const char*>(a.logits) + pos * a.row_stride * nvs::dtype_size(DT);
+        const uint32_t theta_key = r.theta == -INFINITY ? 0u : nvs::float_key(r.theta);
+        const float mu = (r.m == -INFINITY) ? 0.f : r.m;
+        const bool unit_temp = (r.temp == 1.f);
+        uint64_t best = 0;
+        for (int64_t i = threadIdx.x; i < a.vocab; i += blockDim.x) {
+            const float sc = scale_logit(nvs::load_as_float<DT>(row, i), r.temp, unit_temp);
+            const float p = (sel_key(sc) >= theta_key && sc == sc) ? expf(sc - mu) / r.z : 0.f;
+            const float w = bonus ? p : fmaxf(p - q_at(i), 0.f);
+            const float score = w / erow[i];
+            const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+                                 static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i));
+            best = best > k64 ? best : k64;
+        }
+        best = block_max_u64(best, sh);
+        if (threadIdx.x == 0) {
+            a.n_accept[b] = n;
+            a.tail[b] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(best));
+            a.counters[b] = 0;  // ready for the next call
+        }
+    }
+}
+
+// Positions of a batch row that has L verified positions from `start` and was located by a workgroup (L >= 1,
+// start < n_pos): each of them counts itself once, so the row's counter reaches exactly this and is reset by the
+// finish. Lengths that run past the logits (lens summing to more than n_pos) count only the positions that exist,
+// so the counter never stays non-zero for the next call.
+__device__ __forceinline__ int64_t row_positions(const SelArgs& a, int64_t start, int64_t L) {
+    return min(L, a.n_pos - start);
+}
+
+// Count a finished position of batch row b on the row's counter; the position that counts last finishes the row.
+// Returns whether this position counted last. The caller stored its record with store_record: the wait below
+// holds the add back until those stores are performed at the coherence point, and the finishing workgroup issues
+// its record loads (load_record, also at the coherence point) only after its own add has returned, so it reads
+// every record of the row.
+__device__ __forceinline__ bool count_position(int* counter, int64_t n_positions) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): every store of this wave has completed
+    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return before == static_cast<int>(n_positions) - 1;
+}
+
+// The end of one vocabulary chunk of a race spread over (row, chunk) workgroups, run by wave 0 of the chunk's
+// workgroup: lane 0 publishes the chunk's best key to the row's partials at the coherence point and counts the
+// chunk on the row's counter (count_position); the workgroup that counts last reads every chunk's key of the row
+// (one load per lane, at the coherence point), resets the counter for the next call and returns true with the
+// row's best key in winner. Every lane of wave 0 must call it; the result is uniform over the wave.
+__device__ __forceinline__ bool finish_race_chunk(uint64_t* row_partials, int n_chunks, int c, uint64_t key,
+                                                  int* counter, uint64_t& winner) {
+    const int lane = threadIdx.x & 63;
+    int last = 0;
+    if (lane == 0) {
+        __hip_atomic_store(row_partials + c, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = count_position(counter, n_chunks) ? 1 : 0;
+    }
+    last = __builtin_amdgcn_readfirstlane(last);
+    if (!last) return false;
+    uint64_t best = 0;
+    for (int j = lane; j < n_chunks; j += 64) {
+        const uint64_t v = __hip_atomic_load(row_partials + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        best = best > v ? best : v;
+    }
+    winner = wave_max_u64(best);
+    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
 }
 
 // ---------------------------------------------------------------- Markov draw (DSpark candidate rows)
@@ -1647,6 +1813,11 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         const float zz = (m == -INFINITY) ? 0.f : z * expf(m - mu);
         rs.z = block_sum(zz, sh);
         rs.m = mall;
+    } else if (K > kMaxTopK) {
+        // a window wider than the candidate lists (the first bound below covers at most kMaxTopK): the exact path
+        // over the row decides every truncating row of the batch, the wide ones without any list
+        load_decision();
+        rs = exact_row_stats<DT, VEC>(a, row, temp, unit_temp, rank, K, top_p, sh);
     } else {
         // ---- one pass: every element >= tau, a lower bound of the K-th largest, joins a candidate list private
         // to its lane: kLaneCap slots, slot s of lane l of wave w at sh.ckey[w * kWaveSlots + s * 64 + l] (the
@@ -2048,8 +2219,8 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                         r.race = winner;
                         store_record(a.rec + t, r);
                         if (sh.found) {
-                            const int64_t L_eff = min(max(L, int64_t{1}), static_cast<int64_t>(kd) + 1);
-                            sh.last = count_position(&a.counters[b], L_eff) ? 1 : 0;
+                            // every position of the row that exists counts once (see row_positions)
+                            sh.last = count_position(&a.counters[b], row_positions(a, sh.loc[3], L)) ? 1 : 0;
                         }
                     }
                 }
@@ -2239,10 +2410,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             r.race = winner;
             store_record(a.rec + t, r);
             // count the position; the row's last position to arrive finishes the row
-            if (sh.found) {
-                const int64_t L_eff = min(max(L, int64_t{1}), static_cast<int64_t>(kd) + 1);
-                sh.last = count_position(&a.counters[b], L_eff) ? 1 : 0;
-            }
+            if (sh.found) sh.last = count_position(&a.counters[b], row_positions(a, sh.loc[3], L)) ? 1 : 0;
         }
         __syncthreads();
         if (!sh.last) return;
@@ -2467,9 +2635,9 @@ int check_dtype(int dt) {
     return NVS_OK;
 }
 
+// Any window width is served: windows above kMaxTopK take the exact path over the row (wide_row_stats).
 int check_topk(int max_top_k) {
     NVS_CHECK(max_top_k >= 0, NVS_ERR_INVALID, "sampler: max_top_k %d is negative", max_top_k);
-    NVS_CHECK(max_top_k <= kMaxTopK, NVS_ERR_UNSUPPORTED, "sampler: max_top_k %d above %d", max_top_k, kMaxTopK);
     return NVS_OK;
 }
 
@@ -2657,6 +2825,7 @@ extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t log
     st = common_select_checks(logits, logits_row_stride, batch, vocab, 1, max_top_k, top_k);
     if (st != NVS_OK) return st;
     NVS_CHECK(max_top_k >= 1, NVS_ERR_INVALID, "markov_draw: candidate rows need top-k (max_top_k >= 1)");
+    NVS_CHECK(max_top_k <= kMaxTopK, NVS_ERR_UNSUPPORTED, "markov_draw: max_top_k %d above %d", max_top_k, kMaxTopK);
     NVS_CHECK(num_candidates <= kMaxCandidates, NVS_ERR_UNSUPPORTED,
               "markov_draw: num_candidates %d above %d", num_candidates, kMaxCandidates);
     NVS_CHECK(num_candidates >= 1 && num_candidates >= min(static_cast<int64_t>(max_top_k), vocab), NVS_ERR_INVALID,
@@ -3084,6 +3253,27 @@ static int spec_accept_impl(const void* logits, int logits_dtype, int64_t logits
     return nvs::check_launch("spec_accept dense race");
 }
 
+namespace nvs {
+
+size_t spec_accept_workspace_bytes(int64_t batch, int64_t n_pos, int64_t vocab, int max_top_k) {
+    return accept_layout(batch, n_pos, vocab, max_top_k == 0).bytes;
+}
+
+int spec_accept_dense_q(const void* logits, int logits_dtype, int64_t logits_row_stride, const float* temperatures,
+                        const int64_t* top_k, const float* top_p, int max_top_k, int has_top_p, const float* q,
+                        const int64_t* drafts, const int64_t* verified_lens, const float* uniforms,
+                        const float* noise, int64_t batch, int num_drafts, int64_t n_pos, int64_t vocab,
+                        int64_t* n_accept, int64_t* tail, int32_t* row_counters, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+    NVS_CHECK(q != nullptr || batch == 0, NVS_ERR_INVALID, "spec_accept: q is NULL");
+    return spec_accept_impl(logits, logits_dtype, logits_row_stride, temperatures, top_k, top_p, max_top_k,
+                            has_top_p, q, nullptr, nullptr, 0, 0, drafts, verified_lens, uniforms, noise, batch,
+                            num_drafts, n_pos, vocab, n_accept, tail, row_counters, workspace, workspace_bytes,
+                            stream);
+}
+
+}  // namespace nvs
+
 extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t logits_row_stride,
                                const float* temperatures, const int64_t* top_k, const float* top_p, int max_top_k,
                                int has_top_p, const float* q, const int64_t* drafts, const int64_t* verified_lens,
@@ -3091,11 +3281,9 @@ extern "C" int nvs_spec_accept(const void* logits, int logits_dtype, int64_t log
                                int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail,
                                int32_t* row_counters, void* workspace, size_t workspace_bytes, void* stream) {
     nvs::clear_error();
-    NVS_CHECK(q != nullptr || batch == 0, NVS_ERR_INVALID, "spec_accept: q is NULL");
-    return spec_accept_impl(logits, logits_dtype, logits_row_stride, temperatures, top_k, top_p, max_top_k,
-                            has_top_p, q, nullptr, nullptr, 0, 0, drafts, verified_lens, uniforms, noise, batch,
-                            num_drafts, n_pos, vocab, n_accept, tail, row_counters, workspace, workspace_bytes,
-                            stream);
+    return nvs::spec_accept_dense_q(logits, logits_dtype, logits_row_stride, temperatures, top_k, top_p, max_top_k,
+                                    has_top_p, q, drafts, verified_lens, uniforms, noise, batch, num_drafts, n_pos,
+                                    vocab, n_accept, tail, row_counters, workspace, workspace_bytes, stream);
 }
 
 extern "C" int nvs_spec_accept_candidates(const void* logits, int logits_dtype, int64_t logits_row_stride,

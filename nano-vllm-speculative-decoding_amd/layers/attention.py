@@ -4,10 +4,12 @@ Mirrors nanovllm/layers/attention.py:
   store_kvcache(key, value, k_cache, v_cache, slot_mapping)          attention.py:33-40
   Attention(num_heads, head_dim, scale, num_kv_heads).forward(q,k,v)  attention.py:43-77
 and the two flash-attn entry points that forward calls, with the keyword arguments it passes:
-  paged_attention_varlen(...)        for flash_attn_varlen_func(..., causal=True, block_table=...) (verify branch)
-  paged_attention_with_kvcache(...)  for flash_attn_with_kvcache(q[B, Lq, H, D], ...) (decode / draft-block branch)
-Both run nvs_paged_attention (one HIP launch; when a row's keys are split, the last split of each unit merges the
-partials inside it) and store_kvcache runs nvs_store_kvcache.
+  flash_attn_varlen_func(..., causal=True, block_table=...)  varlen_func: paged_attention_varlen when a block table
+                                     is given (verify rows), otherwise the prefill function bound before the swap
+  flash_attn_with_kvcache(q[B, Lq, H, D], ...)                paged_attention_with_kvcache (decode / draft block)
+The paged calls run nvs_paged_attention (one HIP launch; when a row's keys are split, the last split of each unit
+merges the partials inside it) and store_kvcache runs nvs_store_kvcache. bind(module) installs all three names on a
+module written like the reference's.
 """
 from __future__ import annotations
 
@@ -127,12 +129,45 @@ def paged_attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ma
                            softmax_scale: float, causal: bool = True,
                            block_table: torch.Tensor | None = None) -> torch.Tensor:
     """The call attention.py:67-70 makes with a block table: k, v are the paged caches [blocks, bs, Hkv, D];
-    row r owns queries cu_seqlens_q[r]..cu_seqlens_q[r+1] and cu_seqlens_k[r+1]-cu_seqlens_k[r] keys."""
+    row r owns queries cu_seqlens_q[r]..cu_seqlens_q[r+1] and cu_seqlens_k[r+1]-cu_seqlens_k[r] keys.
+    A call without a block table (k, v = the new rows of a prompt) is not paged attention: see varlen_func."""
     if block_table is None:
-        raise NotImplementedError("nvs_amd implements the paged (block_table) verify branch only; prefill "
-                                  "attention without a prefix cache is outside the verify hot path")
+        raise NotImplementedError("paged_attention_varlen needs a block table; a prefill without a cached prefix "
+                                  "goes to the prefill attention that varlen_func(prefill) forwards it to")
     return _paged_attention(q, k, v, block_table, cu_seqlens_q, cu_seqlens_k, None, 0, cu_seqlens_q.numel() - 1,
                             max_seqlen_q, max_seqlen_k, softmax_scale, causal)
+
+
+def varlen_func(prefill=None):
+    """A flash_attn_varlen_func for the module-level name Attention.forward calls (attention.py:67-70).
+
+    The reference calls that one name for two different things:
+      * block_table given (verify rows, prefill over a cached prefix): k, v are the paged caches. This runs
+        nvs_paged_attention (paged_attention_varlen).
+      * block_table None (prefill of prompts with no cached prefix, model_runner.py:176-185, and the runner's
+        warm-up): k, v are the prompt's own new rows [N, Hkv, D], dense and unpaged. That is prompt attention, not
+        the verify path, and it is handed unchanged to `prefill`: the function the name was bound to before the
+        swap (flash-attn's, or any function with its signature).
+    With prefill None such a call raises NotImplementedError."""
+
+    def flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu_seqlens_k,
+                               softmax_scale=None, causal=False, block_table=None, **kwargs):
+        if block_table is None:
+            if prefill is None:
+                raise NotImplementedError("a prefill without a block table needs the prefill attention this name "
+                                          "was bound to before the swap: bind(module) or varlen_func(prefill)")
+            return prefill(q, k, v, max_seqlen_q=max_seqlen_q, cu_seqlens_q=cu_seqlens_q, max_seqlen_k=max_seqlen_k,
+                           cu_seqlens_k=cu_seqlens_k, softmax_scale=softmax_scale, causal=causal,
+                           block_table=None, **kwargs)
+        if kwargs:
+            raise TypeError(f"paged attention takes no further arguments, got {sorted(kwargs)}")
+        if softmax_scale is None:
+            softmax_scale = q.shape[-1] ** -0.5
+        return paged_attention_varlen(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu_seqlens_k,
+                                      softmax_scale, causal, block_table)
+
+    flash_attn_varlen_func.prefill = prefill
+    return flash_attn_varlen_func
 
 
 def paged_attention_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -149,9 +184,42 @@ def paged_attention_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache
     return out.view(B, Lq, H, D)
 
 
-# The names Attention.forward calls in the reference, for a one-line import swap at that call site.
-flash_attn_varlen_func = paged_attention_varlen
+# The names Attention.forward calls in the reference. This module's own Attention looks them up here at call time,
+# so they can be rebound (set_prefill_attention, or a test's monkeypatch) as the reference's module attributes can.
+flash_attn_varlen_func = varlen_func(None)
 flash_attn_with_kvcache = paged_attention_with_kvcache
+
+_BOUND_NAMES = ("store_kvcache", "flash_attn_varlen_func", "flash_attn_with_kvcache")
+
+
+def bind(module) -> dict:
+    """Swap the attention names of a module written like nanovllm/layers/attention.py for this library's.
+
+    module.store_kvcache          -> store_kvcache (nvs_store_kvcache); DFlashDraftModel.store_context_kv calls it
+                                     through the module attribute too (dflash.py:95)
+    module.flash_attn_with_kvcache -> paged_attention_with_kvcache (nvs_paged_attention, fixed-Lq mode)
+    module.flash_attn_varlen_func  -> varlen_func(previous): paged calls run nvs_paged_attention, calls without a
+                                     block table keep going to the function bound there before
+    Binding twice keeps the first prefill function. Returns the previous bindings (for unbind)."""
+    previous = {name: getattr(module, name, None) for name in _BOUND_NAMES}
+    prefill = previous["flash_attn_varlen_func"]
+    prefill = getattr(prefill, "prefill", prefill)    # already bound: keep the prefill it forwards to
+    module.store_kvcache = store_kvcache
+    module.flash_attn_varlen_func = varlen_func(prefill)
+    module.flash_attn_with_kvcache = paged_attention_with_kvcache
+    return previous
+
+
+def unbind(module, previous: dict) -> None:
+    """Restore the bindings bind() returned."""
+    for name, value in previous.items():
+        setattr(module, name, value)
+
+
+def set_prefill_attention(prefill) -> None:
+    """Where this module's own Attention sends prefill calls without a block table (None: they raise)."""
+    global flash_attn_varlen_func
+    flash_attn_varlen_func = varlen_func(prefill)
 
 
 class Attention(nn.Module):
@@ -166,22 +234,22 @@ class Attention(nn.Module):
         self.k_cache = self.v_cache = torch.tensor([])
 
     def forward(self, q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | None) -> torch.Tensor:
-        """k = v = None: the new K/V rows are already in the cache (qk_norm_rope_store wrote them)."""
+        """k = v = None: the new K/V rows are already in the cache (qk_norm_rope_store wrote them).
+        The three kernels are the module-level names store_kvcache / flash_attn_varlen_func /
+        flash_attn_with_kvcache, looked up at call time."""
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
         if k is not None and k_cache.numel() and v_cache.numel():
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
         if context.is_prefill:
-            if context.block_tables is None:
-                raise NotImplementedError("nvs_amd Attention serves the paged verify / decode branches; prefill "
-                                          "without a prefix cache is outside the verify hot path")
-            return paged_attention_varlen(q, k_cache, v_cache, max_seqlen_q=context.max_seqlen_q,
-                                          cu_seqlens_q=context.cu_seqlens_q, max_seqlen_k=context.max_seqlen_k,
-                                          cu_seqlens_k=context.cu_seqlens_k, softmax_scale=self.scale, causal=True,
-                                          block_table=context.block_tables)
-        # decode: query_len_per_seq queries per sequence, sequence-major rows
-        o = paged_attention_with_kvcache(q.view(-1, context.query_len_per_seq, self.num_heads, self.head_dim),
-                                         k_cache, v_cache, cache_seqlens=context.context_lens,
-                                         block_table=context.block_tables, softmax_scale=self.scale,
-                                         causal=context.causal)
+            paged = context.block_tables is not None      # a cached prefix: attend over the pages
+            return flash_attn_varlen_func(q, k_cache if paged else k, v_cache if paged else v,
+                                          max_seqlen_q=context.max_seqlen_q, cu_seqlens_q=context.cu_seqlens_q,
+                                          max_seqlen_k=context.max_seqlen_k, cu_seqlens_k=context.cu_seqlens_k,
+                                          softmax_scale=self.scale, causal=True, block_table=context.block_tables)
+        # decode / draft block: query_len_per_seq queries per sequence, rows grouped by sequence
+        o = flash_attn_with_kvcache(q.view(-1, context.query_len_per_seq, self.num_heads, self.head_dim),
+                                    k_cache, v_cache, cache_seqlens=context.context_lens,
+                                    block_table=context.block_tables, softmax_scale=self.scale,
+                                    causal=context.causal)
         return o.view(-1, self.num_heads, self.head_dim)

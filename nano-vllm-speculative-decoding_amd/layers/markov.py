@@ -20,6 +20,9 @@ from .. import _lib
 from . import spec_sampler as ss
 
 TIE_MARGIN = 64
+# The widest top-k window nvs_markov_draw serves; wider batches draw their candidate rows with torch's topk and this
+# library's probs_from_logits and race, as the reference composes them (speculative.py:178-181).
+MARKOV_DRAW_MAX_TOP_K = 1024
 
 
 def num_candidates(max_top_k: int, all_top_k: bool, vocab: int) -> int:
@@ -95,10 +98,17 @@ def markov_rows(logits: torch.Tensor, prev: torch.Tensor, sampling: ss.SamplingT
                              torch.empty(batch, k, candidates, dtype=torch.float32, device=logits.device))
     q = None if greedy or candidates else torch.empty(batch, k, vocab, dtype=torch.float32, device=logits.device)
     for row in range(k):
-        if candidates and not greedy:
+        if candidates and not greedy and sampling.max_top_k <= MARKOV_DRAW_MAX_TOP_K:
             # the kernel reads the row of the block's logits and the bias, and adds them itself
             markov_draw(logits[:, row], sampling, candidates, noise[:, row], rows.ids[:, row], rows.probs[:, row],
                         drafts[:, row], bias=markov_bias(prev))
+        elif candidates and not greedy:
+            # a window wider than the kernel's: the row's top `candidates` logits as the candidate row
+            values, ids = (logits[:, row] + markov_bias(prev)).topk(candidates, dim=-1)
+            probs = ss.probs_from_logits(values, sampling)
+            drafts[:, row] = ids.gather(-1, ss.race(probs, noise[:, row]).unsqueeze(-1)).squeeze(-1)
+            rows.ids[:, row] = ids.to(torch.int32)
+            rows.probs[:, row] = probs
         else:
             row_logits = logits[:, row] + markov_bias(prev)
             if greedy:

@@ -27,45 +27,58 @@ NEGATIVE_INFINITY = float("-inf")
 
 @dataclass
 class SamplingTensors:
-    temperatures: torch.Tensor | None  # [B] fp32; None when every row is greedy
-    top_k: torch.Tensor                # [B] int64; 0 disables top-k for that row
-    top_p: torch.Tensor                # [B] fp32; 1.0 disables top-p for that row
-    max_top_k: int                     # host copy of max(top_k); 0 means no row truncates
-    has_top_p: bool                    # host: some row has top_p < 1
-    all_top_k: bool                    # host: every row has top_k > 0
+    """One batch's per-row sampling parameters on the device, with the host-side summaries that size the kernels'
+    launches (the reference's SamplingTensors, spec_sampler.py:17-24: same fields, same meaning).
+
+    temperatures  fp32 [B]; None for a batch that decodes greedily throughout
+    top_k         int64 [B]; a row with 0 keeps its whole vocabulary
+    top_p         fp32 [B]; a row with 1.0 keeps its whole top-k window
+    max_top_k     the batch's largest top_k, known on the host (0: no row truncates)
+    has_top_p     True when at least one row's top_p is below 1
+    all_top_k     True when every row truncates to a top-k window
+    """
+    temperatures: torch.Tensor | None
+    top_k: torch.Tensor
+    top_p: torch.Tensor
+    max_top_k: int
+    has_top_p: bool
+    all_top_k: bool
 
 
 def sampling_tensors(seqs, device: torch.device) -> SamplingTensors:
-    """Per-row parameters of a batch (spec_sampler.py:27-41); mixing greedy and random rows is a ValueError."""
-    temperatures = [seq.temperature for seq in seqs]
-    is_greedy = temperatures[0] == 0
-    if any((temperature == 0) != is_greedy for temperature in temperatures):
+    """The parameters of a batch of sequences (spec_sampler.py:27-41). A batch is either all greedy (temperature 0)
+    or all random; a mixture raises the reference's ValueError."""
+    greedy = {seq.temperature == 0 for seq in seqs}
+    if len(greedy) > 1:
         raise ValueError("mixed greedy and random sampling is not supported")
     top_k = [seq.top_k for seq in seqs]
     top_p = [seq.top_p for seq in seqs]
+    all_greedy = seqs[0].temperature == 0
     return SamplingTensors(
-        temperatures=None if is_greedy else _to_device(temperatures, torch.float32, device),
-        top_k=_to_device(top_k, torch.int64, device),
-        top_p=_to_device(top_p, torch.float32, device),
+        temperatures=None if all_greedy else _upload([seq.temperature for seq in seqs], torch.float32, device),
+        top_k=_upload(top_k, torch.int64, device),
+        top_p=_upload(top_p, torch.float32, device),
         max_top_k=max(top_k),
-        has_top_p=any(value < 1.0 for value in top_p),
+        has_top_p=min(top_p) < 1.0,
         all_top_k=min(top_k) > 0,
     )
 
 
 def sampling_per_token(sampling: SamplingTensors, verified_lens: torch.Tensor, num_tokens: int) -> SamplingTensors:
-    """Each row's parameters repeated over its verified positions, [B] -> [num_tokens] (spec_sampler.py:44-52)."""
-    temperatures = sampling.temperatures
-    return replace(sampling,
-                   temperatures=None if temperatures is None else
-                   temperatures.repeat_interleave(verified_lens, output_size=num_tokens),
-                   top_k=sampling.top_k.repeat_interleave(verified_lens, output_size=num_tokens),
-                   top_p=sampling.top_p.repeat_interleave(verified_lens, output_size=num_tokens))
+    """The same parameters spread from rows to positions, [B] -> [num_tokens]: row r's values repeated
+    verified_lens[r] times, for the flat [T, V] logits of a variable-length verification (spec_sampler.py:44-52).
+    The host summaries do not change."""
+    def spread(per_row: torch.Tensor) -> torch.Tensor:
+        return per_row.repeat_interleave(verified_lens, output_size=num_tokens)
+
+    return replace(sampling, top_k=spread(sampling.top_k), top_p=spread(sampling.top_p),
+                   temperatures=None if sampling.temperatures is None else spread(sampling.temperatures))
 
 
-def _to_device(values: list, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
-    host = torch.tensor(values, dtype=dtype, pin_memory=device.type == "cuda")
-    return host.to(device, non_blocking=True)
+def _upload(values: list, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """A host list as a device tensor, staged in pinned memory so the copy does not block the host."""
+    staged = torch.tensor(values, dtype=dtype, pin_memory=(device.type == "cuda"))
+    return staged.to(device, non_blocking=True)
 
 
 def _rows_view(x: torch.Tensor) -> tuple[torch.Tensor, int, int]:
@@ -273,6 +286,32 @@ def _q_tensor(draft_probs):
     return draft_probs.ids if hasattr(draft_probs, "ids") else draft_probs
 
 
+def accept(target_logits: torch.Tensor, drafts: torch.Tensor, draft_probs, sampling: SamplingTensors,
+           verified_lens: torch.Tensor | list[int] | None,
+           generator: torch.Generator | None) -> tuple[torch.Tensor, torch.Tensor]:
+    """The acceptance step of a speculative round, SpeculativeDecoder._accept (speculative.py:450-462), as one call.
+
+    Which rule runs depends on the batch: greedy (sampling.temperatures is None) or random, and whether every row
+    verifies all k drafts (verified_lens None, target_logits [B, k+1, V]) or row r only its first
+    verified_lens[r] - 1 (target_logits [T, V], T = sum(verified_lens)):
+        greedy, all drafts      accept_greedy(target_logits, drafts)
+        greedy, variable        accept_greedy_varlen(target_logits, drafts, lens)
+        random, all drafts      accept_from_logits(..., None, generator): accept_random(probs_from_logits(...))
+        random, variable        accept_from_logits(..., lens, generator): accept_random_varlen(probs_from_logits(
+                                  logits, sampling_per_token(...)), ...)
+    The random rows run the fused one-launch accept, which reads the logits once and maps positions to rows
+    itself (so the per-token parameters are never built), and draws rand(B, k) then exponential_([B, V]) from
+    `generator`, as the reference does. Greedy rows draw nothing. verified_lens may be a host list (copied to the
+    device as _accept copies it) or a [B] int64 device tensor. Returns (n_accept [B], tail [B]), int64."""
+    if verified_lens is not None and not isinstance(verified_lens, torch.Tensor):
+        verified_lens = _upload(list(verified_lens), torch.int64, target_logits.device)
+    if sampling.temperatures is None:
+        if verified_lens is None:
+            return accept_greedy(target_logits, drafts)
+        return accept_greedy_varlen(target_logits, drafts, verified_lens)
+    return accept_from_logits(target_logits, draft_probs, drafts, sampling, verified_lens, generator)
+
+
 def accept_from_logits(target_logits: torch.Tensor, draft_probs: torch.Tensor, drafts: torch.Tensor,
                        sampling: SamplingTensors, verified_lens: torch.Tensor | None,
                        generator: torch.Generator | None) -> tuple[torch.Tensor, torch.Tensor]:
@@ -329,7 +368,7 @@ def spec_accept_with_draws(target_logits: torch.Tensor, draft_probs: torch.Tenso
                "spec_accept_workspace_size")
     if workspace is None or workspace.numel() < nbytes.value:
         workspace = _lib.workspace(max(nbytes.value, 1), target_logits.device)
-    counters = _lib.persistent_workspace("spec_accept_row_counters", 4 * batch_size, target_logits.device)
+    counters = _row_counters("spec_accept_row_counters", batch_size, target_logits.device)
     if candidates:
         _lib.check(lib.nvs_spec_accept_candidates(
             rows.data_ptr(), _lib.dtype_code(rows.dtype), row_stride, temps.data_ptr(), top_k.data_ptr(),

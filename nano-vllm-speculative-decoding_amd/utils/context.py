@@ -10,6 +10,11 @@ import torch
 
 @dataclass(slots=True)
 class Context:
+    """The field order is the positional order of set_context, which the reference's runner and verify graphs
+    call positionally. query_len_per_seq: how many query rows each sequence contributes on the decode branch (1
+    for plain decoding, the block length when a drafter scores a whole draft block). causal: whether query i of a
+    sequence is limited to keys up to its own position (bottom-right aligned); a draft block sees all its keys and
+    sets it False."""
     is_prefill: bool = False
     cu_seqlens_q: torch.Tensor | None = None
     cu_seqlens_k: torch.Tensor | None = None
@@ -18,8 +23,8 @@ class Context:
     slot_mapping: torch.Tensor | None = None
     context_lens: torch.Tensor | None = None
     block_tables: torch.Tensor | None = None
-    query_len_per_seq: int = 1    # decode queries per sequence; a draft block passes its block size
-    causal: bool = True           # a draft block attends to its whole block: False
+    query_len_per_seq: int = 1
+    causal: bool = True
 
 
 _CONTEXT = Context()

@@ -139,43 +139,46 @@ def verify_varlen_metadata(batch: VerifyBatch | None, num_rows: int, num_tokens:
     k_len - q_len .. k_len - 1 and their cache slots), then padding rows of at most query_len tokens at positions
     0.. of the pad block with slot -1, until num_tokens tokens are placed, then empty rows up to num_rows.
     batch None: every row slot is padding (what a graph is captured on)."""
-    md = VerifyMetadata()
-    rows = [] if batch is None else list(zip(batch.q_lens, batch.k_lens, batch.block_tables))
     if pad_block is None:
         assert batch is not None, "a capture batch needs the pad block"
         pad_block = batch.pad_block
     block_size = 256 if batch is None else batch.block_size
-    if len(rows) > num_rows:
-        raise ValueError(f"{len(rows)} rows do not fit {num_rows} row slots")
+    real = [] if batch is None else list(zip(batch.q_lens, batch.k_lens, batch.block_tables))
+    if len(real) > num_rows:
+        raise ValueError(f"{len(real)} rows do not fit {num_rows} row slots")
+    # What the batch leaves of num_tokens is shared out over the padding rows, query_len tokens at most each.
+    spare = num_tokens - sum(q_len for q_len, _, _ in real)
+    if spare < 0:
+        raise ValueError(f"{num_tokens - spare} tokens do not fit a graph of {num_tokens}")
+    pad_rows = num_rows - len(real)
+    if spare > pad_rows * query_len:
+        raise ValueError(f"{spare} tokens beyond the batch need more than {pad_rows} padding rows of {query_len}")
+    pad_lens = [min(query_len, max(0, spare - i * query_len)) for i in range(pad_rows)]
+
+    md = VerifyMetadata()
+
+    def add_row(first_position: int, n: int, n_keys: int, slots: list[int], table_row: list[int]) -> None:
+        md.positions.extend(range(first_position, first_position + n))
+        md.slot_mapping.extend(slots)
+        md.cu_seqlens_q.append(md.cu_seqlens_q[-1] + n)
+        md.cu_seqlens_k.append(md.cu_seqlens_k[-1] + n_keys)
+        md.block_tables.append(table_row)
+
     num_drafts = query_len - 1
-    for r, (q_len, k_len, table) in enumerate(rows):
-        start = k_len - q_len
+    for r, (q_len, k_len, table) in enumerate(real):
         if not 1 <= q_len <= query_len or len(table) > width or len(table) * block_size < k_len:
             raise ValueError("a row's verify length, context or block table does not fit the graph")
-        first = len(md.positions)
-        last = batch.last_tokens[r] if batch.last_tokens is not None else 0
-        md.input_ids.extend([last] + [0] * (q_len - 1))
-        md.draft_index.extend(range(first + 1, first + q_len))
+        first = len(md.input_ids)
+        md.input_ids.append(batch.last_tokens[r] if batch.last_tokens is not None else 0)
+        md.input_ids.extend([0] * (q_len - 1))
+        md.draft_index.extend(range(first + 1, first + q_len))          # the row's drafts follow its last token
         md.draft_source.extend(range(r * num_drafts, r * num_drafts + q_len - 1))
-        md.positions.extend(range(start, k_len))
-        md.slot_mapping.extend(table[p // block_size] * block_size + p % block_size for p in range(start, k_len))
-        md.cu_seqlens_q.append(md.cu_seqlens_q[-1] + q_len)
-        md.cu_seqlens_k.append(md.cu_seqlens_k[-1] + k_len)
-        md.block_tables.append(table + [pad_block] * (width - len(table)))
-    left = num_tokens - len(md.positions)
-    if left < 0:
-        raise ValueError(f"{len(md.positions)} tokens do not fit a graph of {num_tokens}")
-    for _ in range(num_rows - len(rows)):
-        n = min(left, query_len)
-        left -= n
+        start = k_len - q_len
+        add_row(start, q_len, k_len, [table[p // block_size] * block_size + p % block_size for p in range(start, k_len)],
+                table + [pad_block] * (width - len(table)))
+    for n in pad_lens:   # padding rows attend to their own tokens on the pad block; empty rows have none
         md.input_ids.extend([0] * n)
-        md.positions.extend(range(n))
-        md.slot_mapping.extend([PAD_SLOT] * n)
-        md.cu_seqlens_q.append(md.cu_seqlens_q[-1] + n)
-        md.cu_seqlens_k.append(md.cu_seqlens_k[-1] + n)
-        md.block_tables.append([pad_block] * width)
-    if left:
-        raise ValueError("the padding rows cannot hold the tokens left")
+        add_row(0, n, n, [PAD_SLOT] * n, [pad_block] * width)
     return md
 
 

@@ -291,3 +291,56 @@ def qk_rope_case(num_tokens: int, num_heads: int = 32, num_kv_heads: int = 8, he
     k_cache = torch.zeros(blocks, block_size, num_kv_heads, head_dim, dtype=dtype)
     return QkRopeCase(qkv, positions, q_w, k_w, table, slots, k_cache, torch.zeros_like(k_cache), num_heads,
                       num_kv_heads, head_dim)
+
+
+@dataclass
+class RoundDrafts:
+    """The draft side of a synthetic verify round: drafts [B, k] int64, their dense draft probabilities q [B, k, V]
+    fp32, and per row how many leading drafts follow the target (follow[b] <= q_lens[b] - 1)."""
+    drafts: torch.Tensor
+    q: torch.Tensor
+    follow: list[int]
+
+
+def partly_accepted_drafts(graphs, batch, sampling, num_drafts: int = 7, seed: int = 13) -> RoundDrafts:
+    """Drafts for one verify round on `graphs` (verify_round.VerifyGraphs) that the target partly accepts, so the
+    accept's every branch runs: rows whose verified drafts all follow the target (the bonus token), rows that
+    follow it up to a cut and then carry a random draft (a rejection, then the residual), and rows of random drafts.
+
+    The random drafter draws from a top-64 softmax of N(0, 9) logits. A draft that follows the target is the
+    target's argmax at its position, and its q row is the target's own probabilities there (sampling's per-row
+    parameters), so u * q(d) < p(d) for every u < 1. The forward is causal, so position j's logits depend only on
+    the drafts before j: the drafts are fixed position by position, one forward each. Sets batch.last_tokens."""
+    import random
+
+    from .layers import spec_sampler as ns
+
+    target = graphs.target
+    dev, vocab = target.device, target.shape.vocab_size
+    rows, k = len(batch.q_lens), num_drafts
+    rng = random.Random(seed)
+    follow = []
+    for L in batch.q_lens:
+        kind = rng.choice(("all", "cut", "none"))
+        follow.append(L - 1 if kind == "all" else (rng.randint(0, L - 2) if kind == "cut" and L >= 2 else 0))
+    g = torch.Generator(device=dev).manual_seed(seed)
+    batch.last_tokens = torch.randint(0, vocab, (rows,), generator=torch.Generator().manual_seed(seed)).tolist()
+    q = torch.randn(rows, k, vocab, device=dev, generator=g).mul_(3.0)
+    kth = q.topk(64, dim=-1).values[..., -1:]
+    q = torch.softmax(q.masked_fill_(q < kth, float("-inf")), dim=-1)
+    drafts = (q / torch.empty_like(q).exponential_(generator=g)).argmax(-1)
+    starts = [sum(batch.q_lens[:b]) for b in range(rows)]
+    for j in range(k):
+        chosen = [b for b in range(rows) if j < follow[b]]
+        if not chosen:
+            continue
+        logits = target.compute_logits(graphs.run_drafts(batch, drafts))
+        at = torch.tensor([starts[b] + j for b in chosen], device=dev)
+        drafts[torch.tensor(chosen, device=dev), j] = logits[at].argmax(-1)
+    logits = target.compute_logits(graphs.run_drafts(batch, drafts))
+    lens = torch.tensor(batch.q_lens, dtype=torch.int64, device=dev)
+    p = ns.probs_from_logits(logits, ns.sampling_per_token(sampling, lens, logits.shape[0]))
+    for b in range(rows):
+        for j in range(follow[b]):
+            q[b, j] = p[starts[b] + j]
+    return RoundDrafts(drafts, q, follow)

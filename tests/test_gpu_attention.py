@@ -120,6 +120,37 @@ def test_c3_full_size(device):
     check(run_varlen(c, device, max_seqlen_k=4096), c)
 
 
+@pytest.mark.parametrize("shape", ["c2", "c3", "split"])
+def test_fp16_caches(device, shape):
+    """A model built in fp16 (model_runner.py:55-57 takes hf_config.dtype) runs the same kernel on fp16 q / K / V
+    with the fp16 32x32x16 MFMA and fp16 output: the batch-8 and batch-64 verify layers, and two long rows whose
+    keys are split and merged in the launch, against the fp64 oracle of the same fp16 inputs."""
+    log_case(f"attention fp16 {shape}")
+    if shape == "c2":
+        c = wl.config_c2(torch.float16)
+        out = run_varlen(c, device)
+    elif shape == "c3":
+        c = wl.config_c3(torch.float16)
+        out = run_varlen(c, device, max_seqlen_k=4096)
+    else:
+        c = wl.verify_attention_case([8, 4], [4096, 3001], 32, 8, 128, dtype=torch.float16)
+        out = run_varlen(c, device)
+    check(out, c)
+
+
+def test_fp16_decode_branch(device):
+    log_case("attention fp16 decode branch lq=7 non-causal")
+    ctx = [12, 300, 1025, 64]
+    c = wl.verify_attention_case([7] * 4, ctx, 32, 8, 128, pad_tokens_to=1, dtype=torch.float16)
+    g = c.to(device)
+    out = nattn.paged_attention_with_kvcache(g.q.view(4, 7, 32, 128), g.k_cache, g.v_cache,
+                                             cache_seqlens=torch.tensor(ctx, dtype=torch.int32, device=device),
+                                             block_table=g.block_tables, softmax_scale=g.scale, causal=False)
+    assert out.dtype == torch.float16
+    check(out.view(-1, 32, 128).float().cpu(), c, causal=False,
+          rows=ref.row_layout(context_lens=ctx, query_len_per_seq=7))
+
+
 def test_gqa_group_8_uses_two_query_tiles(device):
     log_case("attention group 8 (64 q heads / 8 kv) lq 8")
     c = wl.verify_attention_case([8, 5], [600, 129], 64, 8, 128)

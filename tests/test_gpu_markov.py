@@ -217,3 +217,19 @@ def test_markov_rows_replay_in_a_graph(device):
         torch.cuda.synchronize()
         assert torch.equal(got[0], want_drafts), f"replay {replay}: drafts differ from the eager rows"
         assert torch.equal(got[1], want.ids) and torch.equal(got[2], want.probs), f"replay {replay}: candidate rows"
+
+
+def test_wide_window_rows_follow_the_oracle(device):
+    """max_top_k above the draw kernel's 1024: each row's candidates come from torch's topk and are drawn with this
+    library's probs_from_logits and race (speculative.py:178-181). The draws equal the oracle's and the candidate
+    rows scatter to the oracle's dense q."""
+    log_case("markov wide window (top-k 1500-3000)")
+    gen = torch.Generator().manual_seed(7)
+    batch, k, vocab = 4, 3, 151936
+    logits = torch.randn(batch, k, vocab, generator=gen) * 3
+    table = torch.randn(64, vocab, generator=gen)
+    anchors = torch.randint(0, vocab, (batch,), generator=gen)
+    st = sampling(device, [1.0, 0.8, 1.0, 1.2], [2000, 1500, 3000, 2000], [1.0, 0.9, 1.0, 0.95])
+    drafts, q, want = run_both(device, logits, anchors, table, st)
+    assert torch.equal(drafts, want[0])
+    torch.testing.assert_close(q.to_dense(vocab).cpu(), want[1], rtol=1e-5, atol=1e-7)

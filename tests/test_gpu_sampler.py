@@ -10,6 +10,7 @@ import json
 import math
 import pathlib
 
+import numpy as np
 import pytest
 import torch
 
@@ -192,11 +193,47 @@ def test_massive_ties_take_the_exact_path(device):
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-7)
 
 
-def margin_report(case, n_got, n_want):
-    """Relative gap of every decision that differs; a genuine bug shows large gaps."""
+def fp32_ulps(a: float, b: float) -> float:
+    """|a - b| in units in the last place (fp32) of the larger magnitude."""
+    big = max(abs(a), abs(b))
+    return 0.0 if big == 0.0 else abs(a - b) / float(np.spacing(np.float32(big)))
+
+
+def margin_report(case, n_got, n_want, tail_got=None, tail_want=None):
+    """For every batch row whose accepted length or tail differs from the oracle's, how close the oracle's own
+    decisions were to a tie, in fp32 ulps: each verified draft's accept test u * q(d) < p(d) (spec_sampler.py:142),
+    and the race at the row's tail position, the gap between its two best scores w / E (spec_sampler.py:106,
+    w = p at the bonus position, else max(p - q, 0)). A legitimate flip (the kernel's exp and sums round apart from
+    torch's CPU ones) shows a gap of a few ulps at the decision that differs; a bug shows a large one."""
+    logits = case.logits.float()
+    batch, k = case.drafts.shape
+    lens = case.verified_lens if case.verified_lens is not None else torch.full((batch,), k + 1, dtype=torch.int64)
+    starts = torch.cumsum(lens, 0) - lens
+    t, tk, tp = (x.repeat_interleave(lens) for x in (case.temperatures, case.top_k, case.top_p))
+    p = ref.probs_from_logits(logits, t, tk, tp, case.max_top_k, case.has_top_p)
+    bad = n_got != n_want
+    if tail_got is not None:
+        bad |= tail_got != tail_want
     lines = []
-    for b in torch.nonzero(n_got != n_want).flatten().tolist():
-        lines.append(f"row {b}: n_accept {int(n_got[b])} vs {int(n_want[b])}")
+    for b in torch.nonzero(bad).flatten().tolist():
+        s, L = int(starts[b]), int(lens[b])
+        head = f"row {b}: n_accept {int(n_got[b])} vs {int(n_want[b])}"
+        if tail_got is not None:
+            head += f", tail {int(tail_got[b])} vs {int(tail_want[b])}"
+        lines.append(head)
+        for j in range(min(L - 1, k)):
+            d = int(case.drafts[b, j])
+            uq = float(case.uniforms[b, j]) * float(case.q[b, j, d])
+            pd = float(p[s + j, d])
+            lines.append(f"  draft {j} (token {d}): u*q = {uq:.9g}, p = {pd:.9g}, accepted {uq < pd}, "
+                         f"gap {fp32_ulps(uq, pd):.1f} ulps")
+        n = int(n_want[b])
+        w = p[s + n] if n == L - 1 else torch.clamp(p[s + n] - case.q[b, min(n, k - 1)], min=0.0)
+        scores = w / case.noise[b]
+        top = scores.topk(2)
+        lines.append(f"  race at position {s + n}: best {int(top.indices[0])} ({float(top.values[0]):.9g}), "
+                     f"second {int(top.indices[1])} ({float(top.values[1]):.9g}), "
+                     f"gap {fp32_ulps(float(top.values[0]), float(top.values[1])):.1f} ulps")
     return "\n".join(lines)
 
 
@@ -237,8 +274,8 @@ def test_fused_accept_is_bit_exact(device, name, kwargs):
     case = wl.sampler_case(draft_probs_fn=draft_probs, **kwargs)
     n_got, tail_got = run_fused(case, device)
     n_want, tail_want = run_oracle(case)
-    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want)
-    assert torch.equal(tail_got, tail_want)
+    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want, tail_got, tail_want)
+    assert torch.equal(tail_got, tail_want), margin_report(case, n_got, n_want, tail_got, tail_want)
     print(f"{name}: accepted {n_got.float().mean():.2f} of {case.drafts.shape[1]} on average")
 
 
@@ -274,8 +311,8 @@ def test_fused_accept_random_configs_are_bit_exact(device, seed):
     case = wl.sampler_case(draft_probs_fn=draft_probs, **kwargs)
     n_got, tail_got = run_fused(case, device)
     n_want, tail_want = run_oracle(case)
-    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want)
-    assert torch.equal(tail_got, tail_want)
+    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want, tail_got, tail_want)
+    assert torch.equal(tail_got, tail_want), margin_report(case, n_got, n_want, tail_got, tail_want)
 
 
 def nucleus_margin(scaled_row, top_k, top_p, max_top_k):
@@ -367,8 +404,8 @@ def test_fused_accept_bound_refinement_and_exact_fallback(device, kind):
     case = dataclasses.replace(base, logits=ordered_logits(base, kind))
     n_got, tail_got = run_fused(case, device)
     n_want, tail_want = run_oracle(case)
-    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want)
-    assert torch.equal(tail_got, tail_want)
+    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want, tail_got, tail_want)
+    assert torch.equal(tail_got, tail_want), margin_report(case, n_got, n_want, tail_got, tail_want)
 
 
 @pytest.mark.parametrize("top_k", [200, 700])
@@ -379,8 +416,52 @@ def test_fused_accept_large_top_k(device, top_k):
     case = wl.sampler_case(8, 7, 151936, top_k=top_k, draft_probs_fn=draft_probs)
     n_got, tail_got = run_fused(case, device)
     n_want, tail_want = run_oracle(case)
-    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want)
-    assert torch.equal(tail_got, tail_want)
+    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want, tail_got, tail_want)
+    assert torch.equal(tail_got, tail_want), margin_report(case, n_got, n_want, tail_got, tail_want)
+
+
+@pytest.mark.parametrize("top_k, top_p", [(2000, [1.0]), (2000, [0.9, 1.0, 0.5, 0.97]), (151936, [0.95, 1.0]),
+                                          (1 << 30, [1.0])])
+def test_fused_accept_wide_top_k(device, top_k, top_p):
+    """Windows wider than the 1024-value candidate lists (sampling_params.py:15-16 allows any top_k): the rank-th
+    largest by a radix select over the row, top-p by the nucleus-mass radix descent, the race over the row."""
+    log_case(f"fused accept wide top_k {top_k} top_p {top_p}")
+    case = wl.sampler_case(8, 7, 151936, top_k=top_k, top_p=(top_p * 8)[:8], draft_probs_fn=draft_probs)
+    n_got, tail_got = run_fused(case, device)
+    n_want, tail_want = run_oracle(case)
+    assert torch.equal(n_got, n_want), margin_report(case, n_got, n_want, tail_got, tail_want)
+    assert torch.equal(tail_got, tail_want), margin_report(case, n_got, n_want, tail_got, tail_want)
+
+
+@pytest.mark.parametrize("name, top_k, top_p, temp", [
+    ("topk2000", [2000, 1500, 64, 3000], [1.0, 0.9, 1.0, 0.95], [1.0, 0.7]),
+    ("topk_vocab", [1 << 30, 0, 5000, 1 << 30], [0.95, 1.0, 1.0, 1.0], [1.0, 1.3]),
+    ("topk_vocab_no_topp", [1 << 30, 2000], [1.0], [1.0, 0.8]),
+])
+@pytest.mark.parametrize("vocab", [4099, 151936])
+def test_wide_top_k_probs_and_truncation(device, name, top_k, top_p, temp, vocab):
+    """probs_from_logits and truncate_logits with windows past 1024 values, up to the whole vocabulary, against the
+    oracle: the same kept set (a top-p row may cut elsewhere only at a nucleus tie of <= 4 ulps, nucleus_margin),
+    probabilities within 1e-5 relative, truncated logits bit for bit."""
+    log_case(f"wide top-k probs {name} V={vocab}")
+    logits, rows = probs_params(16, vocab, top_k, top_p, temp, seed=len(name) + vocab)
+    st, (t, k, p, mk, hp) = sampling(rows, device)
+    want = ref.probs_from_logits(logits, t, k, p, mk, hp)
+    got = ns.probs_from_logits(logits.to(device), st).cpu()
+    scaled = logits / t[:, None]
+    trunc_want = ref.truncate_logits(scaled, k, p, mk, hp)
+    trunc_got = ns.truncate_logits(scaled.to(device), st).cpu()
+    normal = torch.finfo(torch.float32).tiny
+    for r in range(logits.shape[0]):
+        if not torch.equal(torch.isfinite(trunc_got[r]), torch.isfinite(trunc_want[r])):
+            margin = nucleus_margin(scaled[r], int(k[r]), float(p[r]), mk)
+            assert hp and margin <= 4 * 2.0 ** -23, f"position {r}: kept sets differ with nucleus margin {margin:.3e}"
+            print(f"position {r}: nucleus tie, margin {margin:.3e}")
+            continue
+        assert torch.equal(trunc_got[r], trunc_want[r])
+        differ = (got[r] > 0) != (want[r] > 0)
+        assert bool((got[r][differ] < normal).all() and (want[r][differ] < normal).all())
+        torch.testing.assert_close(got[r], want[r], rtol=1e-5, atol=1e-7)
 
 
 @pytest.mark.parametrize("kind", ["ascending", "rising_trend"])
@@ -426,6 +507,73 @@ def test_fused_accept_repeats_and_replays_in_a_graph(device, top_k):
         assert torch.equal(n_g.cpu(), n_want) and torch.equal(tail_g.cpu(), tail_want)
         n, tail = call()  # eager work between replays
         assert torch.equal(n.cpu(), n_want)
+
+
+def test_graph_captured_before_the_counters_grow(device):
+    """A graph of the fused accept captured while its row counters were small replays correctly after a larger
+    eager call replaced them: a replaced counter buffer stays allocated, and every call leaves it zero."""
+    log_case("fused accept: graph replays after the row counters grew")
+    small = wl.sampler_case(8, 3, 4096, draft_probs_fn=draft_probs)
+    n_want, tail_want = run_oracle(small)
+    g = small.to(device)
+    st = ns.SamplingTensors(g.temperatures, g.top_k, g.top_p, small.max_top_k, small.has_top_p, True)
+
+    def call():
+        return ns.spec_accept_with_draws(g.logits, g.q, g.drafts, st, None, g.uniforms, g.noise)
+
+    call()
+    before = _lib.persistent_workspace("spec_accept_row_counters", 4, torch.device(device))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        n_g, tail_g = call()
+    big = wl.sampler_case(20000, 1, 64, top_k=8, draft_probs_fn=draft_probs)   # past the counters' minimum size
+    n_big, tail_big = run_fused(big, device)
+    n_big_want, tail_big_want = run_oracle(big)
+    assert torch.equal(n_big, n_big_want) and torch.equal(tail_big, tail_big_want)
+    after = _lib.persistent_workspace("spec_accept_row_counters", 4, torch.device(device))
+    assert after.data_ptr() != before.data_ptr() and after.numel() >= 4 * 20000
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(n_g.cpu(), n_want) and torch.equal(tail_g.cpu(), tail_want)
+        assert int(before.view(torch.int32).abs().sum()) == 0
+
+
+@pytest.mark.parametrize("greedy", [False, True], ids=["random", "greedy"])
+@pytest.mark.parametrize("varlen", [False, True], ids=["all_drafts", "varlen"])
+def test_accept_dispatch_follows_the_reference_branches(device, greedy, varlen):
+    """accept() is SpeculativeDecoder._accept (speculative.py:450-462): greedy or random rows, every row verifying
+    all k drafts ([B, k+1, V] logits) or verified_lens[r] - 1 of them ([T, V], lens handed over as the host list
+    _accept receives). Each branch against the oracle's, bit for bit, and the generator left exactly where the
+    reference leaves it: rand(B, k) then exponential_([B, V]) for random rows, untouched for greedy ones."""
+    log_case(f"accept dispatch greedy={greedy} varlen={varlen}")
+    lens = [1, 8, 3, 5, 2, 7, 4, 6] if varlen else None
+    case = wl.sampler_case(8, 7, 32000, top_k=[64, 20, 5, 64] * 2, top_p=[0.9, 1.0, 0.6, 0.95] * 2,
+                           temperature=[0.7, 1.0, 1.5, 1.0] * 2, verified_lens=lens, draft_probs_fn=draft_probs)
+    g = case.to(device)
+    batch, k = case.drafts.shape
+    logits = g.logits if varlen else g.logits.view(batch, k + 1, -1)
+    st = ns.SamplingTensors(None if greedy else g.temperatures, g.top_k, g.top_p, case.max_top_k, case.has_top_p,
+                            True)
+    ours = torch.Generator(device=device).manual_seed(77)
+    n, tail = ns.accept(logits, g.drafts, None if greedy else g.q, st, lens, ours)
+    theirs = torch.Generator(device=device).manual_seed(77)
+    if greedy:
+        want = ref.accept_greedy_varlen(case.logits, case.drafts, case.verified_lens) if varlen else \
+            ref.accept_greedy(case.logits.view(batch, k + 1, -1), case.drafts)
+    else:
+        uniforms = torch.rand(batch, k, device=device, generator=theirs)
+        noise = torch.empty(batch, 32000, device=device).exponential_(1.0, generator=theirs).clamp_min_(1e-10)
+        want = ref.accept_from_logits(case.logits, case.q, case.drafts, case.temperatures, case.top_k, case.top_p,
+                                      case.max_top_k, case.has_top_p, case.verified_lens, uniforms.cpu(),
+                                      noise.cpu())
+    assert torch.equal(ours.get_state(), theirs.get_state())
+    assert torch.equal(n.cpu(), want[0]) and torch.equal(tail.cpu(), want[1])
 
 
 @pytest.mark.parametrize("vocab", [50000, 50001])   # 16-byte pieces / element loads

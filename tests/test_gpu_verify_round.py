@@ -194,3 +194,58 @@ def test_run_drafts_places_the_drafts_like_the_host_layout(device):
         got = graphs.run_drafts(batch, drafts.to(device)).clone()
         torch.cuda.synchronize()
         assert torch.equal(got, want)
+
+
+def test_qwen3_8b_round_at_batch_64(device):
+    """The fifth benchmark configuration as a test: 36 Qwen3-8B-shaped layers (random bf16 weights, paged
+    head-major KV) over 64 rows of 1..8 verified tokens at 2,800-3,200-token contexts, captured as one HIP graph,
+    then the LM head and the accept (speculative.py:411-448 for the round, :450-462 for the accept).
+    The drafts partly follow the target (workloads.partly_accepted_drafts), so rows accept all their drafts (the
+    bonus token), stop at a rejection (the residual), or reject at once. Checked: the graph replay equals the eager
+    forward bit for bit; the fused accept (top-k 64, temperature 1) and the greedy accept on the round's bf16 logits
+    equal the oracle's, bit for bit, given the same uniforms and noise; the generator is left where the
+    reference's accept_random_varlen leaves it; acceptances, bonus tokens and residuals all occur."""
+    import nvs_amd.workloads as wl
+    from nvs_amd.layers import spec_sampler as ns
+    from oracle import spec_sampler as ref_s
+
+    log_case("verify round: 36 Qwen3-8B layers, B 64, q 1-8, ctx 2800-3200, fused and greedy accept")
+    shape = vr.QWEN3_8B
+    batch = vr.random_verify_batch(64)
+    target = vr.Qwen3VerifyTarget(shape, batch.num_blocks, device=device)
+    graphs = vr.VerifyGraphs(target, max_batch_size=512, query_len=8, max_model_len=4096)
+    B, T, V = len(batch.q_lens), batch.num_tokens, shape.vocab_size
+    st = ns.SamplingTensors(torch.ones(B, device=device), torch.full((B,), 64, dtype=torch.int64, device=device),
+                            torch.ones(B, device=device), 64, False, True)
+    rd = wl.partly_accepted_drafts(graphs, batch, st)
+    hidden = graphs.run_drafts(batch, rd.drafts).clone()
+    ids = graphs.input_ids[:T].clone()
+    eager = graphs.run_eager(batch, ids).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(hidden, eager), "graph replay differs from the eager forward"
+    logits = target.compute_logits(hidden)
+    lens = torch.tensor(batch.q_lens, dtype=torch.int64)
+    ours = torch.Generator(device=device).manual_seed(12)
+    n, tail = ns.accept(logits, rd.drafts, rd.q, st, batch.q_lens, ours)
+    theirs = torch.Generator(device=device).manual_seed(12)
+    uniforms = torch.rand(B, 7, device=device, generator=theirs)
+    noise = torch.empty(B, V, device=device).exponential_(1.0, generator=theirs).clamp_min_(1e-10)
+    assert torch.equal(ours.get_state(), theirs.get_state())
+    logits_cpu = logits.float().cpu()
+    n_want, tail_want = ref_s.accept_from_logits(logits_cpu, rd.q.cpu(), rd.drafts.cpu(), torch.ones(B),
+                                                 torch.full((B,), 64, dtype=torch.int64), torch.ones(B), 64, False,
+                                                 lens, uniforms.cpu(), noise.cpu())
+    n, tail = n.cpu(), tail.cpu()
+    assert torch.equal(n, n_want) and torch.equal(tail, tail_want)
+    bonus = n == lens - 1
+    print(f"fused accept: mean accepted {float(n.float().mean()):.2f}, bonus rows {int(bonus.sum())}, "
+          f"rows with a residual {int((~bonus).sum())}, rows following the target {sum(f > 0 for f in rd.follow)}")
+    assert float(n.float().mean()) > 0 and bool(bonus.any()) and bool((~bonus).any())
+    follow = torch.tensor(rd.follow)
+    assert bool((n >= follow).all()), "a draft that follows the target with q = p was rejected"
+    greedy = ns.SamplingTensors(None, st.top_k, st.top_p, 64, False, True)
+    n_g, tail_g = ns.accept(logits, rd.drafts, None, greedy, batch.q_lens, ours)
+    n_gw, tail_gw = ref_s.accept_greedy_varlen(logits_cpu, rd.drafts.cpu(), lens)
+    assert torch.equal(n_g.cpu(), n_gw) and torch.equal(tail_g.cpu(), tail_gw)
+    assert bool((n_g.cpu() >= follow).all())
+    assert torch.equal(ours.get_state(), theirs.get_state()), "the greedy accept drew random numbers"

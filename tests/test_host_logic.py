@@ -68,13 +68,34 @@ def test_store_kvcache_keeps_the_reference_preconditions():
         nattn.store_kvcache(key, key, cache, cache, torch.tensor([0, 1], dtype=torch.int32))
 
 
-def test_prefill_without_block_table_is_out_of_scope():
+def test_unbound_prefill_without_block_table_raises():
+    """With no prefill attention bound, a call without a block table is refused (never run as paged attention);
+    the binding tests (test_attention_binding.py) show where a bound one sends it."""
     with pytest.raises(NotImplementedError):
         nattn.paged_attention_varlen(torch.zeros(1), torch.zeros(1), torch.zeros(1), 1, torch.zeros(2), 1,
                                      torch.zeros(2), 1.0, True, None)
+    with pytest.raises(NotImplementedError):
+        nattn.varlen_func(None)(torch.zeros(1), torch.zeros(1), torch.zeros(1), max_seqlen_q=1,
+                                cu_seqlens_q=torch.zeros(2), max_seqlen_k=1, cu_seqlens_k=torch.zeros(2),
+                                softmax_scale=1.0, causal=True)
 
 
 def test_truncate_without_top_k_returns_the_input():
     s = rows((1.0, 0, 1.0))
     x = torch.randn(2, 5)
     assert ns.truncate_logits(x, s) is x
+
+
+def test_outgrown_persistent_buffers_stay_allocated(monkeypatch):
+    """A counter buffer replaced by a larger one is kept referenced (a graph captured with it still holds its
+    address), and the name now maps to the larger buffer."""
+    from nvs_amd import _lib
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    monkeypatch.setattr(_lib, "_persistent", {})
+    monkeypatch.setattr(_lib, "_superseded", [])
+    dev = torch.device("cpu")
+    small = _lib.persistent_workspace("test_counters", 1000, dev)
+    assert _lib.persistent_workspace("test_counters", 500, dev) is small
+    big = _lib.persistent_workspace("test_counters", 100000, dev)
+    assert big is not small and big.numel() >= 100000 and int(big.sum()) == 0
+    assert any(buf is small for buf in _lib._superseded)
