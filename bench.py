@@ -57,6 +57,24 @@ def time_gpu(fn, steps: int, warmup: int):
     return start.elapsed_time(end) / steps
 
 
+def host_info() -> dict:
+    """What the CPU baselines ran on: the processor model, the cores this process may use, torch's version and
+    thread count."""
+    import torch
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(),
+            "usable_cores": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+            "torch": torch.__version__, "torch_threads": torch.get_num_threads()}
+
+
 def time_cpu(fn, budget_s: float = 15.0, max_runs: int = 10):
     fn()  # warm-up
     times = []
@@ -249,6 +267,7 @@ def sampler_cpu_baseline(case, n_gpu, tail_gpu):
     log(f"[bench] sampler cpu baseline: {sec * 1e3:.1f} ms per call on {torch.get_num_threads()} threads "
         f"(same decisions as the GPU: {same})")
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "host": host_info(),
             "sample": f"the whole 64 x 8 x 151,936 fp32 case (probs_from_logits + accept_random, same draws), "
                       f"median of {runs} runs: {sec * 1e3:.1f} ms per call", "ms_per_call": round(sec * 1e3, 2),
             "same_decisions_as_gpu": same}
@@ -519,6 +538,7 @@ def verify_round_bench(args, dev):
     Floor: the weights (15.14 GB) + 36 layers of K/V + the logits written once and read once, at 8 TB/s."""
     import torch
 
+    import nvs_amd.workloads as wl
     from nvs_amd import verify_round as vr
     from nvs_amd.layers import spec_sampler as ns
 
@@ -530,21 +550,19 @@ def verify_round_bench(args, dev):
     rows, tokens = graphs.shape_for(batch.num_tokens)
     graphs.capture([tokens])
     B, k, V, T = len(batch.q_lens), 7, shape.vocab_size, batch.num_tokens
-    g = torch.Generator(device=dev).manual_seed(11)
-    ids = torch.randint(0, V, (T,), device=dev, generator=g)
-    # the drafter's output: a top-64 softmax of N(0, 9) draft logits, drafts drawn from it
-    q = torch.randn(B, k, V, device=dev, generator=g).mul_(3.0)
-    kth = q.topk(64, dim=-1).values[..., -1:]
-    q = torch.softmax(q.masked_fill_(q < kth, float("-inf")), dim=-1)
-    drafts = (q / torch.empty_like(q).exponential_(generator=g)).argmax(-1)
     lens = torch.tensor(batch.q_lens, dtype=torch.int64, device=dev)
     st = ns.SamplingTensors(torch.ones(B, device=dev), torch.full((B,), 64, dtype=torch.int64, device=dev),
                             torch.ones(B, device=dev), 64, False, True)
+    # drafts that the target partly accepts (some rows all, some up to a cut, some none), so the round's accept
+    # runs its acceptance, bonus and residual branches; the random drafter is a top-64 softmax of N(0, 9) logits
+    log("[bench] drafting a partly accepted round (one forward per draft position)")
+    rd = wl.partly_accepted_drafts(graphs, batch, st, k)
+    drafts, q = rd.drafts, rd.q
     gen = torch.Generator(device=dev).manual_seed(12)
-    hidden = graphs.run(batch, ids)
+    hidden = graphs.run_drafts(batch, drafts)
 
     def whole():
-        h = graphs.run(batch, ids)
+        h = graphs.run_drafts(batch, drafts)
         return ns.accept_from_logits(target.compute_logits(h), q, drafts, st, lens, gen)
 
     def forward_only():
@@ -554,7 +572,7 @@ def verify_round_bench(args, dev):
         ns.accept_from_logits(target.compute_logits(hidden), q, drafts, st, lens, gen)
 
     def greedy_round():   # temperature 0: the argmax accept on the same logits (spec_sampler.py:161-169)
-        h = graphs.run(batch, ids)
+        h = graphs.run_drafts(batch, drafts)
         return ns.accept_greedy_varlen(target.compute_logits(h), drafts, lens)
 
     steps, warm = max(5, args.steps // 10), max(2, args.warmup // 5)
@@ -563,6 +581,7 @@ def verify_round_bench(args, dev):
     ms_tail = time_gpu(tail_only, steps, warm)
     ms_greedy = time_gpu(greedy_round, steps, warm)
     n_accept, _ = whole()
+    n_greedy, _ = greedy_round()
     weights = shape.streamed_weight_bytes()
     kv = shape.num_layers * batch.kv_bytes(shape.num_kv_heads, shape.head_dim)
     logits = 2 * T * V * 2
@@ -576,7 +595,11 @@ def verify_round_bench(args, dev):
             "frac_of_floor": round(floor_ms / ms, 4),
             "floor_bytes": {"weights": weights, "kv": kv, "logits_write_and_read": logits},
             "graph_shape": {"row_slots": rows, "tokens": tokens, "verified_tokens": T},
-            "mean_accepted": round(float(n_accept.float().mean()), 3)}
+            "mean_accepted": round(float(n_accept.float().mean()), 3),
+            "mean_accepted_greedy": round(float(n_greedy.float().mean()), 3),
+            "bonus_rows": int((n_accept == lens - 1).sum()), "rows": B,
+            "drafts": "partly accepted: per row all verified drafts, a prefix, or none follow the target's argmax "
+                      "(q = the target's own probabilities there); the rest drawn from a top-64 random drafter"}
 
 
 def copy_probe(args, dev):
@@ -632,6 +655,7 @@ def cpu_baseline(case, hip_out):
     log(f"[bench] attention numerics: max|GPU - fp64| {err_hip:.2e}, max|CPU fp32 - fp64| {err_t32:.2e} "
         f"(first 4 rows); max|GPU - CPU fp32| over every row {diff_all:.2e} (bound 2e-2)")
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "host": host_info(),
             "sample": f"the whole batch-64 layer (same inputs as the GPU run, fp32), median of {runs} runs: "
                       f"{sec * 1e3:.1f} ms/layer", "ms_per_layer": round(sec * 1e3, 2),
             "numerics": {"max_abs_err_gpu_vs_fp64": err_hip, "max_abs_err_cpu_fp32_vs_fp64": err_t32,

@@ -627,6 +627,18 @@ struct RowStats {
     bool dense;   // kept set not held in the candidate list
 };
 
+// Sum over the workgroup in double, in a fixed order (every thread gets the result).
+__device__ double block_sum_f64(double v, SelShared& sh) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();
+    if (lane_id() == 0) sh.u64red[threadIdx.x >> 6] = static_cast<uint64_t>(__double_as_longlong(v));
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < kSelWaves; ++w) t += __longlong_as_double(static_cast<long long>(sh.u64red[w]));
+    return t;
+}
+
 // ---------------------------------------------------------------- windows wider than the candidate lists
 // A row whose top-k window holds more than kMaxTopK values (top_k up to the vocabulary, sampling_params.py:15-16)
 // keeps nothing in LDS: the rank-th largest value comes from a radix select over the row, the top-p threshold from
@@ -660,11 +672,14 @@ __device__ float wide_top_p_threshold(ForEach for_each, uint32_t thr_key, uint32
                                       float top_p, SelShared& sh) {
     const float thr = nvs::key_float(thr_key);
     const uint32_t copies = static_cast<uint32_t>(rank) - n_gt;
-    float tot = 0.f;
+    // the nucleus denominator over up to the whole vocabulary, summed in double: an fp32 sum of 10^5 terms would
+    // carry relative errors near 1e-6, the size of the mass differences the top-p test resolves
+    double tot_d = 0.0;
     for_each([&](uint32_t key) {
-        if (key > thr_key) tot += expf(nvs::key_float(key) - m);
+        if (key > thr_key) tot_d += static_cast<double>(expf(nvs::key_float(key) - m));
     });
-    tot = block_sum(tot, sh) + static_cast<float>(copies) * expf(thr - m);
+    tot_d = block_sum_f64(tot_d, sh) + static_cast<double>(copies) * static_cast<double>(expf(thr - m));
+    const float tot = static_cast<float>(tot_d);
     // the refinement histograms' space is free on this path: masses, then largest keys; counts in sh.hist
     unsigned long long* hmass = reinterpret_cast<unsigned long long*>(&sh.whist[0][0]);
     uint32_t* hmax = &sh.whist[4][0];
@@ -766,20 +781,24 @@ __device__ RowStats wide_row_stats(const SelArgs& a, const void* row, float temp
     rs.theta = nvs::key_float(thr_key);
     if (a.has_top_p) rs.theta = wide_top_p_threshold(for_each, thr_key, n_gt, rank, rs.m, top_p, sh);
     const uint32_t theta_key = nvs::float_key(rs.theta);
-    float z = 0.f;
+    double z = 0.0;   // in double, as the nucleus denominator above
     for_each([&](uint32_t key) {
-        if (key >= theta_key) z += expf(nvs::key_float(key) - rs.m);
+        if (key >= theta_key) z += static_cast<double>(expf(nvs::key_float(key) - rs.m));
     });
-    rs.z = block_sum(z, sh);
+    rs.z = static_cast<float>(block_sum_f64(z, sh));
     rs.dense = true;
     return rs;
 }
 
 // Full-row exact path (candidate list overflowed): radix select on the row, then rebuild the candidate list.
-template <int DT, bool VEC>
+// WIDE: the kernel serves windows wider than the lists (wide_row_stats), compiled only into the select kernels
+// launched for such batches so that the others keep their registers.
+template <int DT, bool VEC, bool WIDE>
 __device__ RowStats exact_row_stats(const SelArgs& a, const void* row, float temp, bool unit_temp,
                                     int rank, int K, float top_p, SelShared& sh) {
-    if (rank > kMaxTopK) return wide_row_stats<DT, VEC>(a, row, temp, unit_temp, rank, top_p, sh);
+    if constexpr (WIDE) {
+        if (rank > kMaxTopK) return wide_row_stats<DT, VEC>(a, row, temp, unit_temp, rank, top_p, sh);
+    }
     auto for_each = [&](auto&& fn) {
         for (int64_t e0 = 0; e0 < a.vocab; e0 += kBatch) {
             float v[kVpt];
@@ -1689,7 +1708,9 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_merge_kernel(MarkovSpli
                 a.cand_probs + b * a.cand_stride, a.draws + b * a.draws_stride, sh);
 }
 
-template <int DT, int MODE, bool VEC>
+// WIDE: instantiated for batches whose max_top_k exceeds the candidate lists (kMaxTopK); the others never carry
+// the wide path's code.
+template <int DT, int MODE, bool VEC, bool WIDE>
 // At most 128 VGPRs (4 waves per SIMD): two 8-wave workgroups per CU, so the 512 positions of a verify batch
 // run in one round on 256 CUs.
 __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
@@ -1813,11 +1834,6 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         const float zz = (m == -INFINITY) ? 0.f : z * expf(m - mu);
         rs.z = block_sum(zz, sh);
         rs.m = mall;
-    } else if (K > kMaxTopK) {
-        // a window wider than the candidate lists (the first bound below covers at most kMaxTopK): the exact path
-        // over the row decides every truncating row of the batch, the wide ones without any list
-        load_decision();
-        rs = exact_row_stats<DT, VEC>(a, row, temp, unit_temp, rank, K, top_p, sh);
     } else {
         // ---- one pass: every element >= tau, a lower bound of the K-th largest, joins a candidate list private
         // to its lane: kLaneCap slots, slot s of lane l of wave w at sh.ckey[w * kWaveSlots + s * 64 + l] (the
@@ -1836,7 +1852,10 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         float tau = INFINITY;
         int lcnt = 0;           // this lane's list length
         uint32_t hmax = 0u;     // largest key this lane appended
-        bool overflow = false;  // the same on every lane of the wave
+        // the same on every lane of the wave. A window wider than the candidate lists (K > kMaxTopK, beyond the
+        // first bound's reach) starts overflowed: the pass then only streams the row, and the exact path decides
+        // every truncating row of the batch (the wide ones without any list, wide_row_stats)
+        bool overflow = WIDE && K > kMaxTopK;
         // With a positive temperature the pass compares raw values: x / t rounds monotonically in x, so the K-th
         // largest scaled value is the K-th largest raw value divided by t, and the lists are scaled once at the end
         // of the pass instead of every value in it. Two adjacent raw values can divide to the same quotient, so the
@@ -2260,7 +2279,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
         }
         __syncthreads();
         if (exact) {
-            rs = exact_row_stats<DT, VEC>(a, row, temp, unit_temp, rank, K, top_p, sh);
+            rs = exact_row_stats<DT, VEC, WIDE>(a, row, temp, unit_temp, rank, K, top_p, sh);
         } else {
             kept_source = kKeptInLists;
             const int n = sh.count;
@@ -2652,10 +2671,21 @@ bool vector_rows(const void* base, int64_t row_stride, int64_t vocab, int dt) {
 template <int DT, int MODE>
 void launch_select_dt(const SelArgs& a, bool vec, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(a.n_pos));
+    // windows wider than the candidate lists take the wide instantiation (the Markov draw never has them)
+    if constexpr (MODE != kModeMarkov) {
+        if (a.max_top_k > kMaxTopK && a.vocab > kMaxTopK) {
+            if (vec) {
+                hipLaunchKernelGGL((select_kernel<DT, MODE, true, true>), grid, dim3(kSelThreads), 0, s, a);
+            } else {
+                hipLaunchKernelGGL((select_kernel<DT, MODE, false, true>), grid, dim3(kSelThreads), 0, s, a);
+            }
+            return;
+        }
+    }
     if (vec) {
-        hipLaunchKernelGGL((select_kernel<DT, MODE, true>), grid, dim3(kSelThreads), 0, s, a);
+        hipLaunchKernelGGL((select_kernel<DT, MODE, true, false>), grid, dim3(kSelThreads), 0, s, a);
     } else {
-        hipLaunchKernelGGL((select_kernel<DT, MODE, false>), grid, dim3(kSelThreads), 0, s, a);
+        hipLaunchKernelGGL((select_kernel<DT, MODE, false, false>), grid, dim3(kSelThreads), 0, s, a);
     }
 }
 

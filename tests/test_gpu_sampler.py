@@ -315,18 +315,26 @@ def test_fused_accept_random_configs_are_bit_exact(device, seed):
     assert torch.equal(tail_got, tail_want), margin_report(case, n_got, n_want, tail_got, tail_want)
 
 
-def nucleus_margin(scaled_row, top_k, top_p, max_top_k):
+def nucleus_margin(scaled_row, top_k, top_p, max_top_k, with_error=False):
     """How far the reference's nucleus test on one row is from a tie: the smallest |mass_before - top_p| over the
     row's top-k candidates and the total mass (spec_sampler.py:87-93). A kept set may legitimately differ from the
     oracle's only when this is a few ulps: the comparison then turns on the last bits of the fp32 softmax, which
-    the GPU's exp and sum round differently from torch's CPU kernel."""
+    the GPU's exp and sum round differently from torch's CPU kernel.
+    with_error: also the reference's own rounding there, the largest |mass_before(fp32) - mass_before(fp64)| over
+    the window. Over a window of 10^5 values torch's fp32 softmax sum alone is off by ~1e-6, so a flip is also
+    legitimate when the margin is within that error (the kernel's sums are kept in double on such windows)."""
     K = min(max_top_k, scaled_row.numel())
     cand = scaled_row.topk(K).values.clone()
     cand[max(top_k, 1):] = float("-inf")
     nucleus = torch.softmax(cand, dim=-1)
     cum = nucleus.cumsum(dim=-1)
     before = (cum - nucleus)[:max(top_k, 1)]
-    return float(torch.cat([before, cum[-1:]]).sub(top_p).abs().min())
+    margin = float(torch.cat([before, cum[-1:]]).sub(top_p).abs().min())
+    if not with_error:
+        return margin
+    nucleus64 = torch.softmax(cand.double(), dim=-1)
+    before64 = (nucleus64.cumsum(dim=-1) - nucleus64)[:max(top_k, 1)]
+    return margin, float((before.double() - before64).abs().max())
 
 
 @pytest.mark.parametrize("seed", range(8))
@@ -454,14 +462,23 @@ def test_wide_top_k_probs_and_truncation(device, name, top_k, top_p, temp, vocab
     normal = torch.finfo(torch.float32).tiny
     for r in range(logits.shape[0]):
         if not torch.equal(torch.isfinite(trunc_got[r]), torch.isfinite(trunc_want[r])):
-            margin = nucleus_margin(scaled[r], int(k[r]), float(p[r]), mk)
-            assert hp and margin <= 4 * 2.0 ** -23, f"position {r}: kept sets differ with nucleus margin {margin:.3e}"
-            print(f"position {r}: nucleus tie, margin {margin:.3e}")
+            margin, err = nucleus_margin(scaled[r], int(k[r]), float(p[r]), mk, with_error=True)
+            assert hp and margin <= 4 * 2.0 ** -23 + 2 * err, \
+                f"position {r}: kept sets differ with nucleus margin {margin:.3e} (reference rounding {err:.3e})"
+            print(f"position {r}: nucleus tie, margin {margin:.3e}, reference rounding {err:.3e}")
             continue
         assert torch.equal(trunc_got[r], trunc_want[r])
         differ = (got[r] > 0) != (want[r] > 0)
         assert bool((got[r][differ] < normal).all() and (want[r][differ] < normal).all())
-        torch.testing.assert_close(got[r], want[r], rtol=1e-5, atol=1e-7)
+        # the probabilities against the fp64 softmax of the same kept set (the kernel sums in double here), and
+        # against the oracle within the oracle's own error against that fp64 softmax
+        kept = torch.isfinite(trunc_want[r])
+        p64 = torch.softmax(scaled[r].double().masked_fill(~kept, float("-inf")), dim=0)
+        live = p64 > 1e-30
+        ref_rel = float(((want[r].double() - p64).abs() / p64.clamp_min(1e-300))[live].max())
+        if int(k[r]) > 0:   # the truncating rows' sums are exact to fp32 (double on wide windows)
+            torch.testing.assert_close(got[r].double()[live], p64[live], rtol=1e-5, atol=0.0)
+        torch.testing.assert_close(got[r], want[r], rtol=max(1e-5, 2 * ref_rel), atol=1e-7)
 
 
 @pytest.mark.parametrize("kind", ["ascending", "rising_trend"])
