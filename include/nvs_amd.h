@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NVS_ABI_VERSION 7
+#define NVS_ABI_VERSION 8
 
 typedef enum {
     NVS_OK = 0,
@@ -240,6 +240,21 @@ int nvs_spec_accept_candidates(const void* logits, int logits_dtype, int64_t log
                                const float* uniforms, const float* noise, int64_t batch, int num_drafts,
                                int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail,
                                int32_t* row_counters, void* workspace, size_t workspace_bytes, void* stream);
+
+/* nvs_spec_accept with no workspace and no row counters from the caller. It has no counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture, serving loops or harnesses
+ * that forbid allocation). The records, dense-race state and per-row counters live in a fixed device array of the
+ * library (1 MiB + 4 KiB per device, held until the process ends), resolved per device on the first call.
+ * Same arguments and results as nvs_spec_accept otherwise. Limits: batch <= 1024 and at most 1 MiB of records
+ * (32 bytes per verify position, plus the dense races' state when max_top_k == 0); larger calls return
+ * NVS_ERR_UNSUPPORTED before any launch. All calls on one device share the array: calls that overlap on a device
+ * (other streams, other host threads) race; calls ordered on one stream do not. Each call clears its row counters
+ * with a kernel first (no memset node, so it can be captured). */
+int nvs_spec_accept_noalloc(const void* logits, int logits_dtype, int64_t logits_row_stride,
+                            const float* temperatures, const int64_t* top_k, const float* top_p, int max_top_k,
+                            int has_top_p, const float* q, const int64_t* drafts, const int64_t* verified_lens,
+                            const float* uniforms, const float* noise, int64_t batch, int num_drafts,
+                            int64_t n_pos, int64_t vocab, int64_t* n_accept, int64_t* tail, void* stream);
 
 /* ------------------------------------------------------------------------------------------------ Markov draw
  * Replaces one candidate row of DFlashDrafter._markov_rows (nanovllm/engine/speculative.py:163-184, the

@@ -56,6 +56,8 @@ SIGNATURES = {
                         _p, _p, ctypes.c_size_t, _p],
     "nvs_spec_accept_candidates": [_p, _i32, _i64, _p, _p, _p, _i32, _i32, _p, _p, _i32, _i64, _p, _p, _p, _p, _i64,
                                    _i32, _i64, _i64, _p, _p, _p, _p, ctypes.c_size_t, _p],
+    "nvs_spec_accept_noalloc": [_p, _i32, _i64, _p, _p, _p, _i32, _i32, _p, _p, _p, _p, _p, _i64, _i32, _i64, _i64,
+                                _p, _p, _p],
     "nvs_markov_draw_workspace_size": [_i64, _i64, _i32, _size_p],
     "nvs_markov_draw": [_p, _i32, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _i32, _i32, _p, _i64, _p, _p, _i64,
                         _p, _i64, _p, ctypes.c_size_t, _p],
