@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NVS_ABI_VERSION 8
+#define NVS_ABI_VERSION 9
 
 typedef enum {
     NVS_OK = 0,
@@ -273,16 +273,18 @@ int nvs_spec_accept_noalloc(const void* logits, int logits_dtype, int64_t logits
  * logits and bias [batch, vocab] fp32 / bf16 / fp16 (one dtype) with row strides; noise [batch, >= num_candidates]
  * fp32, the row's exponential noise by candidate rank; parameters per row as in nvs_probs_from_logits.
  * min(max_top_k, vocab) <= num_candidates <= 7168; batch <= 65535. Up to 512 candidates the row is cut into
- * segments drawn by separate workgroups and merged (workspace: nvs_markov_draw_workspace_size bytes, no
- * initialisation); above 512 one workgroup draws each row, needs no workspace, and takes no bias (add it first).
+ * segments drawn by separate workgroups of one launch, and the row's last segment to finish merges them
+ * (workspace: nvs_markov_draw_workspace_size bytes, no initialisation; row_counters: int32 [batch], zero on the
+ * first call and left zero by every call, shared only by calls ordered on one stream); above 512 one workgroup
+ * draws each row, needs no workspace or counters, and takes no bias (add it first).
  * The rows of a draft block are sequential launches because each row's bias depends on the token drawn before it. */
 int nvs_markov_draw_workspace_size(int64_t batch, int64_t vocab, int num_candidates, size_t* bytes);
 int nvs_markov_draw(const void* logits, int logits_dtype, int64_t logits_row_stride, const void* bias,
                     int64_t bias_row_stride, int64_t batch, int64_t vocab, const float* temperatures,
                     const int64_t* top_k, const float* top_p, int max_top_k, int has_top_p, int num_candidates,
                     const float* noise, int64_t noise_row_stride, int32_t* cand_ids, float* cand_probs,
-                    int64_t cand_row_stride, int64_t* draws, int64_t draws_stride, void* workspace,
-                    size_t workspace_bytes, void* stream);
+                    int64_t cand_row_stride, int64_t* draws, int64_t draws_stride, int32_t* row_counters,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------ decoder-layer elementwise ops
  * The elementwise steps between the projections of a Qwen3 decoder layer, so that a whole verify forward runs

@@ -9,4 +9,4 @@ Every op runs a hand-written HIP kernel from libnvs_amd.so through its C ABI (in
 fallback path: a missing library or a CPU tensor raises.
 """
 __version__ = "0.1.0"
-ABI_VERSION = 8
+ABI_VERSION = 9

@@ -60,7 +60,7 @@ SIGNATURES = {
                                 _p, _p, _p],
     "nvs_markov_draw_workspace_size": [_i64, _i64, _i32, _size_p],
     "nvs_markov_draw": [_p, _i32, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _i32, _i32, _p, _i64, _p, _p, _i64,
-                        _p, _i64, _p, ctypes.c_size_t, _p],
+                        _p, _i64, _p, _p, ctypes.c_size_t, _p],
     "nvs_rms_norm": [_p, _i64, _p, _i64, _p, _f32, _p, _i64, _i64, _i32, _i32, _p],
     "nvs_silu_and_mul": [_p, _i64, _p, _i64, _i64, _i32, _i32, _p],
 }

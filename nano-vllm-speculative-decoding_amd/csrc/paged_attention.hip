@@ -66,6 +66,23 @@ template <> struct Elem16<NVS_DTYPE_F16> {
     static __device__ __forceinline__ uint32_t bits(float f) { return __half_as_ushort(__float2half(f)); }
 };
 
+// Launch shape. kPrefetch: chunks of K/V each wave keeps in flight in registers (a ring, so the loads of the wave's
+// next kPrefetch chunks are outstanding while one chunk is computed); kWgPerCu: resident workgroups per CU, which
+// bounds the registers a wave may hold (256 at 2, 512 at 1).
+#ifndef NVS_ATTN_PREFETCH
+#define NVS_ATTN_PREFETCH 1
+#endif
+#ifndef NVS_ATTN_WG_PER_CU
+#define NVS_ATTN_WG_PER_CU 2
+#endif
+#ifndef NVS_ATTN_ROWS_FIRST
+#define NVS_ATTN_ROWS_FIRST 0
+#endif
+constexpr int kPrefetch = NVS_ATTN_PREFETCH;
+constexpr int kWgPerCu = NVS_ATTN_WG_PER_CU;
+// grid dimension order: (kv head x query tile, row, split), or with rows first (row, kv head x query tile, split)
+constexpr bool kRowsFirst = NVS_ATTN_ROWS_FIRST != 0;
+
 constexpr int kHeadDim = 128;
 constexpr int kTileRows = 32;    // packed query rows per tile
 constexpr int kChunk = 32;       // keys per MFMA chunk
@@ -149,7 +166,7 @@ __device__ __forceinline__ int active_splits(int lk, int split_len) {
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
 template <int DT>
-__global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kThreads, kWgPerCu) void attn_split_kernel(AttnArgs a) {
     using E = Elem16<DT>;
     using V8 = typename E::vec8;
     __shared__ __attribute__((aligned(16))) uint16_t tiles[kWaves * kWaveElems];
@@ -159,9 +176,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
 
     // grid (kv head x query tile, row, split): every unit's first split is dispatched before any second split, so
     // the idle splits of short rows (s >= the row's split count) sit at the end of the dispatch order
-    const int r = blockIdx.y;
-    const int g = blockIdx.x / a.q_tiles;
-    const int qt = blockIdx.x - g * a.q_tiles;
+    const int r = kRowsFirst ? blockIdx.x : blockIdx.y;
+    const int gq = kRowsFirst ? blockIdx.y : blockIdx.x;
+    const int g = gq / a.q_tiles;
+    const int qt = gq - g * a.q_tiles;
     const int s = blockIdx.z;
     const RowInfo ri = row_info(a, r);
     const int n_base = qt * kTileRows;
@@ -204,9 +222,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
         }
     };
 
-    // This wave's first chunk is requested before the query tile, so the two loads are in flight together.
-    u32x4 kr[8], vr[8];
-    if (wave < nch) load_chunk(wave, kr, vr);
+    // This wave's first kPrefetch chunks are requested before the query tile, so they are in flight together.
+    u32x4 kr[kPrefetch][8], vr[kPrefetch][8];
+#pragma unroll
+    for (int d = 0; d < kPrefetch; ++d)
+        if (wave + kWaves * d < nch) load_chunk(wave + kWaves * d, kr[d], vr[d]);
 
     // The query tile -> LDS (zeros for packed rows past the row's Lq): 32 rows x 256 B, one 16 B piece per thread
     // and pass.
@@ -267,7 +287,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
     auto process_chunk = [&](int c, u32x4 (&kr)[8], u32x4 (&vr)[8]) {
         const int tb = k0 + c * kChunk;
         stage_chunk(kr, vr);
-        const int cn = c + kWaves;
+        const int cn = c + kWaves * kPrefetch;
         if (cn < nch) load_chunk(cn, kr, vr);
 
         f32x16 acc = f32x16{};
@@ -320,8 +340,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_split_kernel(AttnArgs a) {
 
     __syncthreads();  // query tile staged
 
-    // This wave's chunks are wave, wave + 4, ...; each one's K and V are in flight while the previous is processed.
-    for (int c = wave; c < nch; c += kWaves) process_chunk(c, kr, vr);
+    // This wave's chunks are wave, wave + 4, ...; chunk c sits in ring slot (c / 4) % kPrefetch, and its slot is
+    // refilled with chunk c + 4 kPrefetch as soon as c is staged. The ring is unrolled so its slots stay registers.
+    for (int c0 = wave; c0 < nch; c0 += kWaves * kPrefetch) {
+#pragma unroll
+        for (int d = 0; d < kPrefetch; ++d) {
+            const int c = c0 + kWaves * d;
+            if (c < nch) process_chunk(c, kr[d], vr[d]);
+        }
+    }
 
     // ---- merge the 4 waves (fixed order, so the result does not depend on timing)
     const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -504,7 +531,7 @@ SplitPlan plan_splits(int n_rows, int n_heads, int n_kv_heads, int max_seqlen_q,
     // the (row, kv head, tile) units fill less than half of that round, and then into enough splits to fill it:
     // measured on batch-8/16/32 verify layers (3k contexts), a split costs its partial and the merge, which a grid
     // of one unsplit workgroup per CU does not win back, while a grid under one workgroup per CU does.
-    constexpr int64_t kRound = 512;
+    constexpr int64_t kRound = 256 * kWgPerCu;
     int64_t want = 1;
     if (units > 0 && units * 2 < kRound) want = (kRound + units - 1) / units;
     const int64_t max_k = max_seqlen_k > 0 ? max_seqlen_k : 1;
@@ -639,7 +666,8 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_token_stride, int64_
     a.q_tiles = plan.q_tiles;
 
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(n_kv_heads * plan.q_tiles, n_rows, plan.n_splits);
+    const dim3 grid = kRowsFirst ? dim3(n_rows, n_kv_heads * plan.q_tiles, plan.n_splits)
+                                 : dim3(n_kv_heads * plan.q_tiles, n_rows, plan.n_splits);
     if (dtype == NVS_DTYPE_BF16) {
         hipLaunchKernelGGL(attn_split_kernel<NVS_DTYPE_BF16>, grid, dim3(kThreads), 0, s, a);
     } else {

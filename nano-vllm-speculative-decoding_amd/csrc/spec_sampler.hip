@@ -1359,16 +1359,20 @@ __device__ void markov_tail(const SelArgs& a, int64_t t, const char* row, float 
 
 // ---------------------------------------------------------------- Markov draw split over segments of the row
 // With one workgroup per sequence a batch of 64 leaves three quarters of the chip idle, so the split draw cuts each
-// row into segments of at most kSegKeys values, one workgroup each (8 at V = 151,936: 512 workgroups).
-// markov_segment_kernel keeps its segment's keys in registers, 40 per thread (the Markov bias added and rounded to
-// the logits' dtype, the temperature applied), and writes its top n_cand (key, index) pairs in (value descending,
-// index ascending) order of selection: range histograms find the n_cand-th largest key, the values above it are
-// taken, and the ties at it in index order. The row's top n_cand are among the union of its segments' top n_cand, so markov_merge_kernel
-// sorts that union, keeps its first n_cand as the candidates and finishes as markov_tail does: the top-k threshold
-// and the nucleus over the candidates (the same functions as probs_from_logits), Z, the race and the outputs.
+// row into segments of at most kSegKeys values, one workgroup each (8 at V = 151,936: 512 workgroups), in one
+// launch (markov_draw_kernel). Each workgroup keeps its segment's keys in registers, 40 per thread (the Markov
+// bias added and rounded to the logits' dtype, the temperature applied), and writes its top n_cand (key, index)
+// pairs in (value descending, index ascending) order: a first bound from ballots over the lanes' largest keys
+// leaves a short list of the keys at or above it (a few hundred), ranked exactly by comparing every pair with
+// every other; a list past kShortCap (massive ties) takes range histograms instead. The row's top n_cand are among
+// the union of its segments' top n_cand: the pairs go to the coherence point, each segment counts itself on the
+// row's counter, and the row's last segment to finish merges the lists (a pair's rank is its place in its own
+// list plus, per other list, the pairs above it) and finishes as markov_tail does: the top-k threshold and the
+// nucleus over the candidates (the same functions as probs_from_logits), Z, the race and the outputs.
 
 constexpr int kSegKeys = 19456;          // values of one segment (at most 40 per thread, kept in registers)
-constexpr int kSplitMaxCand = 512;       // candidates of the split draw (segments x candidates within kPairCap / 2)
+constexpr int kSplitMaxCand = 512;       // candidates of the split draw (one per thread of the merging workgroup)
+constexpr int kShortCap = 1024;          // a segment's short list, ranked pair by pair (past it: histograms)
 
 struct MarkovSplitArgs {
     const void* logits;
@@ -1385,7 +1389,8 @@ struct MarkovSplitArgs {
     int n_cand;
     int seg_len;                 // a multiple of 8
     int n_seg;
-    uint64_t* pairs;             // [batch, n_seg, n_cand]
+    uint64_t* pairs;             // [batch, n_seg, n_cand], written and read at the coherence point
+    int* counters;               // [batch] segments of the row finished; zero between calls
     const float* noise;
     int64_t noise_stride;
     int32_t* cand_ids;
@@ -1400,7 +1405,7 @@ __device__ __forceinline__ float round_to_dtype(float x) {
     if constexpr (DT == NVS_DTYPE_F32) {
         return x;
     } else if constexpr (DT == NVS_DTYPE_BF16) {
-        return nvs::bf16_bits_to_float(nvs::float_to_bf16_bits(x));
+        return static_cast<float>(static_cast<__bf16>(x));   // round to nearest even (one conversion on gfx950)
     } else {
         return __half2float(__float2half_rn(x));
     }
@@ -1417,14 +1422,135 @@ __device__ __forceinline__ float half_of(uint32_t w, int hi) {
     }
 }
 
+// The merge of a row's segment lists by the row's last segment to finish (markov_draw_kernel). The lists, each
+// sorted (value descending, index ascending, zeros of empty slots last), are read at the coherence point into the
+// upper half of the pair space. A pair's rank in the union is its place in its own list plus, for every other
+// list, the number of its pairs above it: binary searches, the lists of a group of eight advanced in lockstep so
+// the searches overlap. Every pair is distinct (one index each), and the first n_cand ranks go straight to their
+// place in the lower half. Then the top-k threshold and the nucleus over those candidates, Z, the race and the
+// outputs, as markov_tail does; each thread's candidate noise is requested before the lists are merged.
+// noise_c (this thread's candidate noise, C <= kSelThreads), tk and top_p were loaded before the row's count.
+__device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float noise_c, int64_t tk, float top_p,
+                                 SelShared& sh) {
+    uint64_t* pairs = pair_buf(sh);
+    const int total = a.n_seg * a.n_cand;
+    const int C = a.n_cand;
+    const uint64_t* src = a.pairs + b * total;
+    uint64_t* all = pairs + kPairCap / 2;
+    // every load issued before any is used: one round trip to the coherence point (total <= kPairCap / 2 pairs)
+    constexpr int kPer = kPairCap / 2 / kSelThreads;
+    uint64_t got[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int i = min(static_cast<int>(threadIdx.x) + r * kSelThreads, total - 1);
+        got[r] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    int nz = 0;
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int i = static_cast<int>(threadIdx.x) + r * kSelThreads;
+        if (i < total) {
+            all[i] = got[r];
+            nz += got[r] != 0ull ? 1 : 0;
+        }
+    }
+    for (int i = threadIdx.x; i < C; i += kSelThreads) pairs[i] = 0ull;
+    nz = static_cast<int>(block_sum(static_cast<float>(nz), sh));   // its barriers publish `all`
+    const int want = min(C, nz);
+    constexpr int kGroup = 8;
+    for (int i = threadIdx.x; i < total; i += kSelThreads) {
+        const uint64_t v = all[i];
+        if (v == 0ull) continue;
+        const int own = i / C;
+        int rank = i - own * C;
+        for (int s0 = 0; s0 < a.n_seg; s0 += kGroup) {
+            int lo[kGroup], hi[kGroup];
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) {
+                lo[u] = 0;
+                hi[u] = (s0 + u < a.n_seg && s0 + u != own) ? C : 0;
+            }
+            for (int len = C; len > 0; len >>= 1) {   // floor(log2 C) + 1 halvings empty every interval
+#pragma unroll
+                for (int u = 0; u < kGroup; ++u) {
+                    if (lo[u] < hi[u]) {
+                        const int mid = (lo[u] + hi[u]) >> 1;
+                        if (all[(s0 + u) * C + mid] > v) {
+                            lo[u] = mid + 1;
+                        } else {
+                            hi[u] = mid;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) rank += lo[u];
+        }
+        if (rank < C) pairs[rank] = v;
+    }
+    __syncthreads();
+    const int real = want;
+    const int K = static_cast<int>(min(static_cast<int64_t>(a.max_top_k), a.vocab));
+    int rank = static_cast<int>(min(tk > 0 ? tk : static_cast<int64_t>(K), static_cast<int64_t>(K)));
+    rank = min(rank, real);
+    uint32_t theta_key = 0xffffffffu;   // no value: nothing kept
+    if (rank > 0) {
+        const uint32_t thr_key = static_cast<uint32_t>(pairs[rank - 1] >> 32);
+        float theta = nvs::key_float(thr_key);
+        if (a.has_top_p) {
+            for (int i = threadIdx.x; i < rank; i += kSelThreads) sh.sortbuf[i] = static_cast<uint32_t>(pairs[i] >> 32);
+            __syncthreads();
+            theta = top_p_threshold(sh, rank, K, top_p, theta);
+        }
+        theta_key = nvs::float_key(theta);
+    }
+    // the kept candidates form a prefix of the sorted pairs
+    int kept = 0;
+    for (int c = threadIdx.x; c < real; c += kSelThreads) kept += (static_cast<uint32_t>(pairs[c] >> 32) >= theta_key) ? 1 : 0;
+    kept = static_cast<int>(block_sum(static_cast<float>(kept), sh));
+    // probabilities exp(s - m) / Z over the kept candidates, the race argmax_c p_c / noise_c (first rank on ties,
+    // rank 0 when every score is zero), the candidate row and the drawn token (markov_emit, one candidate per thread)
+    const int c = threadIdx.x;
+    const float m = kept > 0 ? nvs::key_float(static_cast<uint32_t>(pairs[0] >> 32)) : 0.f;
+    float z = (c < kept) ? expf(nvs::key_float(static_cast<uint32_t>(pairs[c] >> 32)) - m) : 0.f;
+    z = block_sum(z, sh);
+    uint64_t best = 0;
+    if (c < C) {
+        float p = 0.f;
+        int32_t id = -1;
+        if (c < kept) {
+            const uint64_t pr = pairs[c];
+            p = expf(nvs::key_float(static_cast<uint32_t>(pr >> 32)) - m) / z;
+            id = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(pr));
+        }
+        a.cand_ids[b * a.cand_stride + c] = id;
+        a.cand_probs[b * a.cand_stride + c] = p;
+        const float score = p / noise_c;
+        best = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+               static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(c));
+    }
+    best = block_max_u64(best, sh);
+    if (threadIdx.x == 0) {
+        const float score = nvs::key_float(static_cast<uint32_t>(best >> 32));
+        const int win = (score > 0.f) ? static_cast<int>(0xffffffffu - static_cast<uint32_t>(best)) : 0;
+        a.draws[b * a.draws_stride] =
+            win < kept ? static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(pairs[win])) : int64_t{0};
+    }
+}
+
 template <int DT, bool VEC, bool BIAS>
-__global__ __launch_bounds__(kSelThreads, 2) void markov_segment_kernel(MarkovSplitArgs a) {
+__global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplitArgs a) {
 #pragma clang fp contract(off)
-    __shared__ uint32_t hist[256];
-    __shared__ int n_gt;
-    __shared__ uint32_t pick_bin, pick_rem;
-    __shared__ uint64_t seg_pairs[kSplitMaxCand];   // the segment's want pairs, before they are sorted
-    __shared__ uint32_t wbound[kSelWaves], whi[kSelWaves];
+    // One SelShared, its members reused phase by phase: the segment's selection (histogram bins, bounds, the short
+    // list in the pair space), then, in the row's last segment, the merge (pair space, sort buffer, reductions).
+    __shared__ SelShared sh;
+    uint32_t* hist = sh.hist;
+    int& n_gt = sh.bin_count;
+    uint32_t& pick_bin = sh.sel_digit;
+    uint32_t& pick_rem = sh.sel_remaining;
+    uint64_t* seg_pairs = reinterpret_cast<uint64_t*>(sh.sortbuf);   // the histogram path's want pairs, unsorted
+    uint32_t* wbound = sh.wlo;
+    uint32_t* whi = sh.wmax;
     constexpr int W = piece_elems<DT>();
     const int seg = blockIdx.x;
     const int64_t b = blockIdx.y;
@@ -1441,7 +1567,8 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_segment_kernel(MarkovSp
     // every piece of this thread requested before any is used (clamped into the segment, no branch: a load behind
     // a branch is sunk to its use and the requests would go out one round trip at a time)
     constexpr int kMaxPc = (kSegKeys / W + kSelThreads - 1) / kSelThreads;
-    __shared__ int tie_part[kMaxPc][kSelWaves];
+    int (*tie_part)[kSelWaves] = reinterpret_cast<int (*)[kSelWaves]>(&sh.whist[0][0]);
+    static_assert(kMaxPc * kSelWaves <= kSelWaves * 256, "the tie counts must fit the refinement histograms");
     u32x4 raw[kMaxPc];
     u32x4 braw[BIAS ? kMaxPc : 1];
 #pragma unroll
@@ -1544,6 +1671,45 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_segment_kernel(MarkovSp
         lo = min(lo, wbound[w]);
         hi = max(hi, whi[w]);
     }
+    uint64_t* out = a.pairs + (b * a.n_seg + seg) * a.n_cand;
+    // the segment's pairs go to the coherence point, where the row's merging workgroup (any XCD) reads them
+    auto put = [&](int idx, uint64_t v) { __hip_atomic_store(out + idx, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    // The short list: every key at or above the bound (at least want of them; a few hundred for logits of a few
+    // units' spread), appended wave by wave as (key, index) pairs to the pair space.
+    uint64_t* list = pair_buf(sh);
+    if (threadIdx.x == 0) sh.count = 0;
+    __syncthreads();
+    if (want > 0) {
+        const int lane = lane_id();
+        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+        for (int q = 0; q < kMaxPc * W; ++q) {
+            const bool take = q < qlim && kr[q] >= lo;
+            const uint64_t bal = __ballot(take);
+            if (bal == 0ull) continue;
+            int base = 0;
+            if (lane == 0) base = atomicAdd(&sh.count, __popcll(bal));
+            base = __shfl(base, 0);
+            const int p = base + __popcll(bal & below);
+            if (take && p < kShortCap) {
+                const int i = (static_cast<int>(threadIdx.x) + (q / W) * kSelThreads) * W + q % W;
+                list[p] = (static_cast<uint64_t>(kr[q]) << 32) | (0xffffffffu - static_cast<uint32_t>(e_lo + i));
+            }
+        }
+    }
+    __syncthreads();
+    const int nl = sh.count;
+    if (nl <= kShortCap) {
+        // every pair's rank in the list (all pairs differ: one index each); the first want are the segment's
+        for (int p = threadIdx.x; p < nl; p += kSelThreads) {
+            const uint64_t v = list[p];
+            int above = 0;
+            for (int j = 0; j < nl; ++j) above += (list[j] > v) ? 1 : 0;
+            if (above < want) put(above, v);
+        }
+    } else {
+    // Massive ties at the bound: range histograms find the want-th largest key, the keys above it are taken, then
+    // the ties at it in index order.
     uint32_t span = hi - lo;
     uint32_t rank = static_cast<uint32_t>(want);
     for (int pass = 0; pass < 5 && want > 0; ++pass) {
@@ -1572,7 +1738,6 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_segment_kernel(MarkovSp
     }
     const uint32_t prefix = lo;
     const uint32_t t_key = prefix;
-    uint64_t* out = a.pairs + (b * a.n_seg + seg) * a.n_cand;
     // The keys above the threshold (fewer than want) in any order, then the first want - n_gt ties in index
     // order. Ties of each register group are counted per thread, and one workgroup prefix over all groups at once
     // gives every tie its rank.
@@ -1629,84 +1794,36 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_segment_kernel(MarkovSp
         }
         base += total_j;
     }
-    // the segment's list, sorted: each pair goes to its rank among the want pairs (all distinct); empty slots (a
-    // segment with fewer values than candidates) hold 0, below every pair
+    // the segment's list, sorted: each pair goes to its rank among the want pairs (all distinct)
     __syncthreads();
     for (int p = threadIdx.x; p < want; p += kSelThreads) {
         const uint64_t v = seg_pairs[p];
         int above = 0;
         for (int q = 0; q < want; ++q) above += (seg_pairs[q] > v) ? 1 : 0;
-        out[above] = v;
+        put(above, v);
     }
-    for (int p = want + threadIdx.x; p < a.n_cand; p += kSelThreads) out[p] = 0ull;
-}
+    }
+    // empty slots (a segment with fewer values than candidates) hold 0, below every pair
+    for (int p = want + threadIdx.x; p < a.n_cand; p += kSelThreads) put(p, 0ull);
 
-__global__ __launch_bounds__(kSelThreads, 2) void markov_merge_kernel(MarkovSplitArgs a) {
-    __shared__ SelShared sh;
-    const int64_t b = blockIdx.x;
-    uint64_t* pairs = pair_buf(sh);
-    const int total = a.n_seg * a.n_cand;
-    const int C = a.n_cand;
-    // The segments' lists, each sorted (value descending, index ascending, zeros of empty slots last), go to the
-    // upper half of the pair space. A pair's rank in the union is its place in its own list plus, for every other
-    // list, the number of its pairs above it (a binary search): every pair is distinct (one index each). The first
-    // n_cand ranks go straight to their place in the lower half.
-    const uint64_t* src = a.pairs + b * total;
-    uint64_t* all = pairs + kPairCap / 2;
-    int nz = 0;
-    for (int i = threadIdx.x; i < total; i += kSelThreads) {
-        const uint64_t v = src[i];
-        all[i] = v;
-        nz += v != 0ull ? 1 : 0;
-    }
-    for (int i = threadIdx.x; i < C; i += kSelThreads) pairs[i] = 0ull;
-    nz = static_cast<int>(block_sum(static_cast<float>(nz), sh));   // its barriers publish `all`
-    const int want = min(C, nz);
-    for (int i = threadIdx.x; i < total; i += kSelThreads) {
-        const uint64_t v = all[i];
-        if (v == 0ull) continue;
-        const int own = i / C;
-        int rank = i - own * C;
-        for (int s1 = 0; s1 < a.n_seg && rank < C; ++s1) {
-            if (s1 == own) continue;
-            const uint64_t* list = all + s1 * C;
-            int lo = 0, hi = C;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (list[mid] > v) {
-                    lo = mid + 1;
-                } else {
-                    hi = mid;
-                }
-            }
-            rank += lo;
-        }
-        if (rank < C) pairs[rank] = v;
+    // What the merge needs besides the lists, requested now so it arrives during the count's round trip.
+    const float noise_c = threadIdx.x < a.n_cand ? a.noise[b * a.noise_stride + threadIdx.x] : 1.f;
+    const int64_t row_tk = a.top_k[b];
+    const float row_top_p = a.has_top_p ? a.top_p[b] : 1.f;
+    // Count the segment on the row's counter once every wave's stores have completed; the row's last segment to
+    // count merges. Its loads are issued after its own count returned, at the coherence point.
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int before = __hip_atomic_fetch_add(a.counters + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh.last = (before == a.n_seg - 1) ? 1 : 0;
     }
     __syncthreads();
-    const int real = want;
-    const int K = static_cast<int>(min(static_cast<int64_t>(a.max_top_k), a.vocab));
-    const int64_t tk = a.top_k[b];
-    int rank = static_cast<int>(min(tk > 0 ? tk : static_cast<int64_t>(K), static_cast<int64_t>(K)));
-    rank = min(rank, real);
-    uint32_t theta_key = 0xffffffffu;   // no value: nothing kept
-    if (rank > 0) {
-        const uint32_t thr_key = static_cast<uint32_t>(pairs[rank - 1] >> 32);
-        float theta = nvs::key_float(thr_key);
-        if (a.has_top_p) {
-            for (int i = threadIdx.x; i < rank; i += kSelThreads) sh.sortbuf[i] = static_cast<uint32_t>(pairs[i] >> 32);
-            __syncthreads();
-            theta = top_p_threshold(sh, rank, K, a.top_p[b], theta);
-        }
-        theta_key = nvs::float_key(theta);
-    }
-    // the kept candidates form a prefix of the sorted pairs
-    int kept = 0;
-    for (int c = threadIdx.x; c < real; c += kSelThreads) kept += (static_cast<uint32_t>(pairs[c] >> 32) >= theta_key) ? 1 : 0;
-    kept = static_cast<int>(block_sum(static_cast<float>(kept), sh));
-    markov_emit(pairs, kept, C, a.noise + b * a.noise_stride, a.cand_ids + b * a.cand_stride,
-                a.cand_probs + b * a.cand_stride, a.draws + b * a.draws_stride, sh);
+    if (!sh.last) return;
+    if (threadIdx.x == 0) __hip_atomic_store(a.counters + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    markov_merge_row(a, b, noise_c, row_tk, row_top_p, sh);
 }
+
 
 // WIDE: instantiated for batches whose max_top_k exceeds the candidate lists (kMaxTopK); the others never carry
 // the wide path's code.
@@ -2821,15 +2938,14 @@ template <int DT>
 static void launch_markov_split(const MarkovSplitArgs& a, bool vec, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(a.n_seg), static_cast<unsigned>(a.batch));
     if (vec && a.bias) {
-        hipLaunchKernelGGL((markov_segment_kernel<DT, true, true>), grid, dim3(kSelThreads), 0, s, a);
+        hipLaunchKernelGGL((markov_draw_kernel<DT, true, true>), grid, dim3(kSelThreads), 0, s, a);
     } else if (vec) {
-        hipLaunchKernelGGL((markov_segment_kernel<DT, true, false>), grid, dim3(kSelThreads), 0, s, a);
+        hipLaunchKernelGGL((markov_draw_kernel<DT, true, false>), grid, dim3(kSelThreads), 0, s, a);
     } else if (a.bias) {
-        hipLaunchKernelGGL((markov_segment_kernel<DT, false, true>), grid, dim3(kSelThreads), 0, s, a);
+        hipLaunchKernelGGL((markov_draw_kernel<DT, false, true>), grid, dim3(kSelThreads), 0, s, a);
     } else {
-        hipLaunchKernelGGL((markov_segment_kernel<DT, false, false>), grid, dim3(kSelThreads), 0, s, a);
+        hipLaunchKernelGGL((markov_draw_kernel<DT, false, false>), grid, dim3(kSelThreads), 0, s, a);
     }
-    hipLaunchKernelGGL(markov_merge_kernel, dim3(static_cast<unsigned>(a.batch)), dim3(kSelThreads), 0, s, a);
 }
 
 extern "C" int nvs_markov_draw_workspace_size(int64_t batch, int64_t vocab, int num_candidates, size_t* bytes) {
@@ -2848,7 +2964,7 @@ extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t log
                                const int64_t* top_k, const float* top_p, int max_top_k, int has_top_p,
                                int num_candidates, const float* noise, int64_t noise_row_stride, int32_t* cand_ids,
                                float* cand_probs, int64_t cand_row_stride, int64_t* draws, int64_t draws_stride,
-                               void* workspace, size_t workspace_bytes, void* stream) {
+                               int32_t* row_counters, void* workspace, size_t workspace_bytes, void* stream) {
     nvs::clear_error();
     int st = check_dtype(logits_dtype);
     if (st != NVS_OK) return st;
@@ -2878,6 +2994,9 @@ extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t log
         const size_t need = static_cast<size_t>(batch) * m.n_seg * num_candidates * sizeof(uint64_t);
         NVS_CHECK(workspace != nullptr && workspace_bytes >= need, NVS_ERR_WORKSPACE,
                   "markov_draw: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+        NVS_CHECK(row_counters != nullptr, NVS_ERR_INVALID,
+                  "markov_draw: the split draw needs row_counters (int32 [batch], zero between calls)");
+        m.counters = row_counters;
         m.logits = logits;
         m.row_stride = logits_row_stride;
         m.bias = bias;
@@ -2905,7 +3024,7 @@ extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t log
             case NVS_DTYPE_BF16: launch_markov_split<NVS_DTYPE_BF16>(m, vec, s); break;
             default: launch_markov_split<NVS_DTYPE_F16>(m, vec, s); break;
         }
-        return nvs::check_launch("markov draw kernels");
+        return nvs::check_launch("markov draw kernel");
     }
     // more candidates than the split draw takes: one workgroup per sequence, on logits the caller has biased
     NVS_CHECK(bias == nullptr, NVS_ERR_UNSUPPORTED,

@@ -77,12 +77,14 @@ def markov_draw(row_logits: torch.Tensor, sampling: ss.SamplingTensors, candidat
     top_k = ss._contig(sampling.top_k, torch.int64)
     top_p = ss._contig(sampling.top_p, torch.float32)
     ws = _lib.workspace(nbytes.value, row_logits.device)
+    # the split draw's per-row counters (the row's last segment merges), zero between calls
+    counters = ss._row_counters("markov_row_counters", batch, row_logits.device)
     _lib.check(lib.nvs_markov_draw(row_logits.data_ptr(), _lib.dtype_code(row_logits.dtype), row_logits.stride(0),
                                    _lib.ptr(bias), 0 if bias is None else bias.stride(0), batch, vocab,
                                    temps.data_ptr(), top_k.data_ptr(), _lib.ptr(top_p), sampling.max_top_k,
                                    int(sampling.has_top_p), candidates, noise.data_ptr(), noise.stride(0),
                                    ids.data_ptr(), probs.data_ptr(), ids.stride(0), draws.data_ptr(), draws.stride(0),
-                                   _lib.ptr(ws), nbytes.value, _lib.stream_of(row_logits)),
+                                   counters.data_ptr(), _lib.ptr(ws), nbytes.value, _lib.stream_of(row_logits)),
                "markov_draw")
 
 

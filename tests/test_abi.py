@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version_and_empty_error(lib):
-    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 8
+    assert lib.nvs_abi_version() == _lib.ABI_VERSION == 9
     assert isinstance(lib.nvs_last_error(), bytes)
 
 
