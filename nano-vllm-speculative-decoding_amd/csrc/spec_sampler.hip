@@ -1454,41 +1454,46 @@ __device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float nois
             nz += got[r] != 0ull ? 1 : 0;
         }
     }
-    for (int i = threadIdx.x; i < C; i += kSelThreads) pairs[i] = 0ull;
     nz = static_cast<int>(block_sum(static_cast<float>(nz), sh));   // its barriers publish `all`
     const int want = min(C, nz);
-    constexpr int kGroup = 8;
-    for (int i = threadIdx.x; i < total; i += kSelThreads) {
-        const uint64_t v = all[i];
-        if (v == 0ull) continue;
-        const int own = i / C;
-        int rank = i - own * C;
-        for (int s0 = 0; s0 < a.n_seg; s0 += kGroup) {
-            int lo[kGroup], hi[kGroup];
-#pragma unroll
-            for (int u = 0; u < kGroup; ++u) {
-                lo[u] = 0;
-                hi[u] = (s0 + u < a.n_seg && s0 + u != own) ? C : 0;
-            }
-            for (int len = C; len > 0; len >>= 1) {   // floor(log2 C) + 1 halvings empty every interval
-#pragma unroll
-                for (int u = 0; u < kGroup; ++u) {
-                    if (lo[u] < hi[u]) {
-                        const int mid = (lo[u] + hi[u]) >> 1;
-                        if (all[(s0 + u) * C + mid] > v) {
-                            lo[u] = mid + 1;
-                        } else {
-                            hi[u] = mid;
-                        }
-                    }
+    // A tree of pairwise merges, each keeping the top C of its two lists: an element's rank in the merge is its
+    // place in its own list plus the number of the other list's pairs above it (a branch-free binary search). The
+    // nonzero pairs of two lists fill the first ranks, their zeros (empty slots) every rank after them, so every
+    // slot of the output is written. Lists 2m and 2m+1 merge into list m of the other half of the pair space;
+    // a last list without a mate is copied.
+    uint64_t* cur = all;
+    uint64_t* nxt = pairs;
+    for (int n_lists = a.n_seg; n_lists > 1; n_lists = (n_lists + 1) / 2) {
+        for (int e = threadIdx.x; e < n_lists * C; e += kSelThreads) {
+            const int li = e / C;
+            const int i = e - li * C;
+            const uint64_t x = cur[e];
+            const int mate = li ^ 1;
+            int above = 0;
+            if (mate < n_lists) {
+                const uint64_t* other = cur + mate * C;
+                int lo = 0, hi = C;
+                for (int len = C; len > 0; len >>= 1) {   // floor(log2 C) + 1 halvings empty the interval
+                    const int mid = (lo + hi) >> 1;
+                    const bool open = lo < hi;
+                    const bool gt = other[min(mid, C - 1)] > x;
+                    lo = (open && gt) ? mid + 1 : lo;
+                    hi = (open && !gt) ? mid : hi;
                 }
+                above = lo;
             }
-#pragma unroll
-            for (int u = 0; u < kGroup; ++u) rank += lo[u];
+            const int rank = i + above;
+            if (rank < C) nxt[(li >> 1) * C + rank] = x;
         }
-        if (rank < C) pairs[rank] = v;
+        __syncthreads();
+        uint64_t* t = cur;
+        cur = nxt;
+        nxt = t;
     }
-    __syncthreads();
+    if (cur != pairs) {   // the top C of the union into the lower half (an odd number of levels leaves it above)
+        for (int i = threadIdx.x; i < C; i += kSelThreads) pairs[i] = cur[i];
+        __syncthreads();
+    }
     const int real = want;
     const int K = static_cast<int>(min(static_cast<int64_t>(a.max_top_k), a.vocab));
     int rank = static_cast<int>(min(tk > 0 ? tk : static_cast<int64_t>(K), static_cast<int64_t>(K)));
@@ -1680,20 +1685,22 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
     if (threadIdx.x == 0) sh.count = 0;
     __syncthreads();
     if (want > 0) {
-        const int lane = lane_id();
-        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        // each lane's count, one prefix over the wave and one reservation per wave, then the lane's keys in order
+        int mine = 0;
+#pragma unroll
+        for (int q = 0; q < kMaxPc * W; ++q) mine += (q < qlim && kr[q] >= lo) ? 1 : 0;
+        const int incl = wave_scan_incl_dpp(mine);
+        int base = 0;
+        if (lane_id() == 63 && incl > 0) base = atomicAdd(&sh.count, incl);
+        int p = __shfl(base, 63) + incl - mine;
 #pragma unroll
         for (int q = 0; q < kMaxPc * W; ++q) {
-            const bool take = q < qlim && kr[q] >= lo;
-            const uint64_t bal = __ballot(take);
-            if (bal == 0ull) continue;
-            int base = 0;
-            if (lane == 0) base = atomicAdd(&sh.count, __popcll(bal));
-            base = __shfl(base, 0);
-            const int p = base + __popcll(bal & below);
-            if (take && p < kShortCap) {
-                const int i = (static_cast<int>(threadIdx.x) + (q / W) * kSelThreads) * W + q % W;
-                list[p] = (static_cast<uint64_t>(kr[q]) << 32) | (0xffffffffu - static_cast<uint32_t>(e_lo + i));
+            if (q < qlim && kr[q] >= lo) {
+                if (p < kShortCap) {
+                    const int i = (static_cast<int>(threadIdx.x) + (q / W) * kSelThreads) * W + q % W;
+                    list[p] = (static_cast<uint64_t>(kr[q]) << 32) | (0xffffffffu - static_cast<uint32_t>(e_lo + i));
+                }
+                ++p;
             }
         }
     }
