@@ -26,14 +26,17 @@ import time
 HBM_PEAK_GBS = 8000.0
 METRIC = "verify-attn µs/layer & HBM GB/s (% of 8 TB/s) at B=64, 8 q, 3k ctx"
 
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (one counter per run), each scaled
-# by what the counter reads for the 1 GiB copy probe (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); the runs and their
-# numbers are in profiles/hbm_traffic_pmc_verify_attention_and_spec_accept.md. Re-measure after a kernel change.
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (one counter per run) at commit
+# bb85a69, each scaled by what the counter reads for the 1 GiB copy probe (FETCH_SIZE x 1.99995, WRITE_SIZE x 1.0);
+# the runs and their numbers are in profiles/hbm_traffic_pmc_verify_attention_and_spec_accept.md. Re-measure after a
+# kernel change.
 MEASURED_TRAFFIC = {
-    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200": 789_768_455,              # head-major caches
-    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_token_major": 789_781_254,
-    "spec_accept_b64_k7_v151936_fp32_topk64": 320_078_949,
+    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200": 789_788_975,              # head-major caches, bb85a69
+    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_token_major": 789_803_327,  # bb85a69
+    "spec_accept_b64_k7_v151936_fp32_topk64": 320_040_822,                              # bb85a69
+    "markov_draw_b64_v151936_bf16_rank64": 40_863_105,                                  # bb85a69
 }
+MEASURED_AT = "bb85a69"
 
 
 def log(msg: str) -> None:
@@ -534,7 +537,7 @@ def markov_bench(args, dev):
             "draw_us_single_graph": round(ms_d1 * 1e3, 2),
             "draw_GBs": round(alg / (ms_d * 1e-3) / 1e9, 1), "markov_head_gemm_us": round(ms_b * 1e3, 2),
             "candidates": C, "q_bytes_dense": B * k * V * 4, "q_bytes_candidates": B * k * C * 8,
-            "draw_algorithmic_bytes": alg,
+            "draw_algorithmic_bytes": alg, "draw_traffic": MEASURED_TRAFFIC["markov_draw_b64_v151936_bf16_rank64"],
             "kernel": "markov_draw_kernel (one launch per Markov row; the row's last segment merges)"}
 
 
@@ -733,6 +736,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": MEASURED_TRAFFIC["verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200"],
+                     "traffic_measured_at": MEASURED_AT,
                      "bytes_per_launch": nbytes,
                      "kernel": "attn_split_kernel (batch 64 runs unsplit: one launch per paged_attention call)"},
         "mfma_tflops_useful": round(flops / (ms * 1e-3) / 1e12, 2),
