@@ -96,9 +96,9 @@ constexpr int kRowStride = kHeadDim + 8;                 // bf16 elements per st
 constexpr int kTileElems = kChunk * kRowStride;          // one 32-key tile
 constexpr int kWaveElems = 2 * kTileElems;               // K tile + V tile
 constexpr int kObStride = 33;                            // fp32 per dim row of the cross-wave reduction buffer
-// A split's partial is staged in LDS past the reduction buffer: [32 rows][128 dims] fp32 (16-byte pieces swizzled
+static_assert(kWaves * kHeadDim * kObStride * 4 <= kWaves * kWaveElems * 2, "the waves' partials fit the tiles");
+// A split's partial is staged in LDS over the reduction buffer: [32 rows][128 dims] fp32 (16-byte pieces swizzled
 // by row), then the rows' (max, sum) pairs.
-constexpr int kStageOffset = kHeadDim * kObStride;       // in floats
 constexpr int kMaxSplits = 64;                           // the merge keeps [splits][32] (max, sum) pairs in LDS
 // Query tile in LDS: [32 packed rows][128 dims] bf16 with the same padded rows (B-operand reads of 32 rows at one
 // column per half-wave).
@@ -372,37 +372,38 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void attn_split_kernel(AttnArgs
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] *= own;
 
-    float* ob = reinterpret_cast<float*>(tiles);  // the K/V tiles are dead after the barrier above
+    // Every wave stages its scaled partial O in LDS ([wave][dim][row], the K/V tiles are dead after the barrier
+    // above); then wave w sums the four partials of dims 32w .. 32w + 31, in wave order (so the result does not
+    // depend on timing), into the register layout o[w] had. One barrier instead of four sequential passes.
+    float* ob = reinterpret_cast<float*>(tiles);
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-        if (wave == w) {
+    for (int db = 0; db < 4; ++db) {
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int d = 32 * db + 8 * (j >> 2) + 4 * gi + (j & 3);
-                    float v = o[db][j];
-                    if (w > 0) v += ob[d * kObStride + nl];
-                    o[db][j] = v;
-                    if (w < kWaves - 1) ob[d * kObStride + nl] = v;
-                }
-            }
+        for (int j = 0; j < 16; ++j) {
+            const int d = 32 * db + 8 * (j >> 2) + 4 * gi + (j & 3);
+            ob[(wave * kHeadDim + d) * kObStride + nl] = o[db][j];
         }
-        __syncthreads();
+    }
+    __syncthreads();
+    f32x16 osum;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int d = 32 * wave + 8 * (j >> 2) + 4 * gi + (j & 3);
+        float v = ob[d * kObStride + nl];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) v += ob[(w * kHeadDim + d) * kObStride + nl];
+        osum[j] = v;
     }
     if (n_act == 1) {
-        if (wave != kWaves - 1 || !qvalid) return;
+        if (!qvalid) return;
         const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
         uint16_t* op = a.out + static_cast<int64_t>(ri.q0 + qpos) * a.o_ts + static_cast<int64_t>(h) * a.o_hs;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-#pragma unroll
-            for (int jq = 0; jq < 4; ++jq) {
-                const int d = 32 * db + 8 * jq + 4 * gi;
-                const uint32_t lo = E::bits(o[db][4 * jq + 0] * inv) | (E::bits(o[db][4 * jq + 1] * inv) << 16);
-                const uint32_t hi = E::bits(o[db][4 * jq + 2] * inv) | (E::bits(o[db][4 * jq + 3] * inv) << 16);
-                *reinterpret_cast<u32x2*>(op + d) = u32x2{lo, hi};
-            }
+        for (int jq = 0; jq < 4; ++jq) {
+            const int d = 32 * wave + 8 * jq + 4 * gi;
+            const uint32_t lo = E::bits(osum[4 * jq + 0] * inv) | (E::bits(osum[4 * jq + 1] * inv) << 16);
+            const uint32_t hi = E::bits(osum[4 * jq + 2] * inv) | (E::bits(osum[4 * jq + 3] * inv) << 16);
+            *reinterpret_cast<u32x2*>(op + d) = u32x2{lo, hi};
         }
         return;
     }
@@ -412,20 +413,16 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void attn_split_kernel(AttnArgs
     // unit's last split to finish reads it from any XCD.
     const int64_t unit = (static_cast<int64_t>(r) * a.n_kv + g) * a.q_tiles + qt;
     const int64_t pidx = unit * a.n_splits + s;
-    float* stage = reinterpret_cast<float*>(tiles) + kStageOffset;   // past the reduction buffer read above
+    float* stage = reinterpret_cast<float*>(tiles);   // over the partials just read
     float2* stage_ml = reinterpret_cast<float2*>(stage + kTileRows * kHeadDim);
-    if (wave == kWaves - 1) {
+    __syncthreads();   // every wave has read the staged partials before the stage overwrites them
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-#pragma unroll
-            for (int jq = 0; jq < 4; ++jq) {
-                const int d = 32 * db + 8 * jq + 4 * gi;
-                *reinterpret_cast<float4*>(stage + nl * kHeadDim + (d ^ ((nl & 7) << 2))) =
-                    make_float4(o[db][4 * jq], o[db][4 * jq + 1], o[db][4 * jq + 2], o[db][4 * jq + 3]);
-            }
-        }
-        if (gi == 0) stage_ml[nl] = make_float2(m_all, l_all);
+    for (int jq = 0; jq < 4; ++jq) {
+        const int d = 32 * wave + 8 * jq + 4 * gi;
+        *reinterpret_cast<float4*>(stage + nl * kHeadDim + (d ^ ((nl & 7) << 2))) =
+            make_float4(osum[4 * jq], osum[4 * jq + 1], osum[4 * jq + 2], osum[4 * jq + 3]);
     }
+    if (wave == 0 && gi == 0) stage_ml[nl] = make_float2(m_all, l_all);
     __syncthreads();
     {
         uint64_t* po = reinterpret_cast<uint64_t*>(a.part_o + pidx * kTileRows * kHeadDim);
