@@ -6,20 +6,23 @@
 // Selection kernel (one 512-thread workgroup per logit row = verify position):
 //   * one coalesced pass over the row: s = logit / temperature (IEEE division, skipped when it is exactly 1);
 //   * rows that truncate (top_k > 0): every element at or above a running lower bound tau of the row's
-//     max_top_k-th largest value is appended to an LDS candidate list. tau starts from the first 8192 elements:
-//     each wave takes the ceil(K/8)-th largest of its 64 lane maxima, tau is the smallest of the 8, so at least K
-//     elements lie at or above it. When the list passes half its capacity it is pruned to its exact K-th largest.
-//     The list therefore holds every element >= the K-th largest, ties included, and nothing else is needed;
-//   * exact radix select (8-bit digits over the order-preserving key of each float) in LDS gives the row's
-//     rank-th largest value (rank = min(top_k, K)); top-p sorts the candidates above it (bitonic, LDS) and runs
-//     the nucleus softmax / cumsum of truncate_logits; the kept set is {s >= threshold} (ties kept);
+//     max_top_k-th largest value is appended to a lane-private candidate list in LDS. tau starts from the first
+//     8192 elements: each wave takes the ceil(K/8)-th largest of its 64 lane maxima, tau is the smallest of the 8,
+//     so at least K elements lie at or above it. A wave whose lane fills 12 of its 16 slots raises its bound from a
+//     histogram of its lists and drops what falls below it. The lists therefore hold every element >= the K-th
+//     largest, ties included, and nothing else is needed;
+//   * a 256-bin histogram of the listed keys and a count inside the bin holding the rank-th largest give the
+//     threshold (rank = min(top_k, K)); top-p sorts the candidates above it and runs the nucleus softmax / cumsum of
+//     truncate_logits; the kept set is {s >= threshold} (ties kept);
 //   * rows that do not truncate (top_k = 0) keep an online max / sum-exp instead;
-//   * a list that overflows (thousands of tied values) falls back to an exact radix select over the row itself.
+//   * a lane whose list overflows (thousands of tied values, adversarial order) sends the row to an exact radix
+//     select over the row itself; windows wider than the lists (max_top_k > 1024) take that path by design.
 // Then, depending on the entry point: write dense probabilities (probs_from_logits), write truncated logits
 // (truncate_logits), or (fused accept) evaluate this position's accept test u * q[d] < p[d] and its race:
 // argmax over the kept set of w / E with w = p (bonus position) or max(p - q, 0) (first rejection here), reading
-// q and E only at the kept indices. A finalize kernel per batch row counts the accepted prefix and picks the race
-// of the position that follows it (or races over the whole vocabulary for rows that do not truncate).
+// q and E only at the kept indices. The batch row's last position to finish (counted on a per-row counter) counts
+// the accepted prefix and picks the race of the position that follows it; rows that do not truncate race over the
+// whole vocabulary in a second launch.
 #include "nvs_common.hpp"
 #include "spec_accept.hpp"
 
@@ -1424,11 +1427,9 @@ __device__ __forceinline__ float half_of(uint32_t w, int hi) {
 
 // The merge of a row's segment lists by the row's last segment to finish (markov_draw_kernel). The lists, each
 // sorted (value descending, index ascending, zeros of empty slots last), are read at the coherence point into the
-// upper half of the pair space. A pair's rank in the union is its place in its own list plus, for every other
-// list, the number of its pairs above it: binary searches, the lists of a group of eight advanced in lockstep so
-// the searches overlap. Every pair is distinct (one index each), and the first n_cand ranks go straight to their
-// place in the lower half. Then the top-k threshold and the nucleus over those candidates, Z, the race and the
-// outputs, as markov_tail does; each thread's candidate noise is requested before the lists are merged.
+// upper half of the pair space, all loads issued before any is used. A tree of pairwise merges then keeps the top
+// n_cand of each pair of lists until one list is left (every pair is distinct: one index each). Then the top-k
+// threshold and the nucleus over those candidates, Z, the race and the outputs, as markov_tail does.
 // noise_c (this thread's candidate noise, C <= kSelThreads), tk and top_p were loaded before the row's count.
 __device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float noise_c, int64_t tk, float top_p,
                                  SelShared& sh) {
