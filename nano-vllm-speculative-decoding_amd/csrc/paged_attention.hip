@@ -202,24 +202,36 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void attn_split_kernel(AttnArgs
     const int64_t head_off = static_cast<int64_t>(g) * a.c_hs + 8 * ld_piece;
     const int nch = (k1 - k0 + kChunk - 1) / kChunk;
 
-    // K and V of chunk c into registers (clamped into [0, Lk) so a tail chunk never reads outside the row's pages;
-    // a 32-key chunk never straddles a page because block_size is a multiple of 32).
-    auto load_chunk = [&](int c, u32x4 (&kr)[8], u32x4 (&vr)[8]) {
+    // The unit's block-table entries, one per lane (page k0 / block_size + lane), read once. A chunk takes its block
+    // id with one readlane: a load there would put a memory round trip (about a microsecond under this stream) in
+    // front of every chunk's K/V loads. A unit longer than 64 pages reads the table for the pages past them.
+    const int page0 = k0 / a.block_size;
+    const int bt_lane = btr[min(page0 + lane, a.bt_width - 1)];
+    // Element offset of chunk c's first key in the cache (the same for K and V), the block id clamped into the cache.
+    auto chunk_base = [&](int c) -> int64_t {
         const int tb = k0 + c * kChunk;
         const int page = min(tb / a.block_size, a.bt_width - 1);
-        int64_t blk = btr[page];
+        const int rel = page - page0;
+        int64_t blk = static_cast<unsigned>(rel) < 64u ? __builtin_amdgcn_readlane(bt_lane, rel) : btr[page];
         blk = blk < 0 ? 0 : (blk >= a.n_blocks ? a.n_blocks - 1 : blk);
-        const int64_t base = blk * a.c_bs + head_off;
         const int in_page = tb - (tb / a.block_size) * a.block_size;
+        return blk * a.c_bs + head_off + static_cast<int64_t>(in_page) * a.c_ts;
+    };
+    // Piece i of chunk c: key 4i + ld_key (clamped into [0, Lk) so a tail chunk never reads outside the row's pages;
+    // a 32-key chunk never straddles a page because block_size is a multiple of 32), 16 B of K and of V.
+    auto load_piece = [&](int c, int64_t base, int i, u32x4& kq, u32x4& vq) {
+        const int tb = k0 + c * kChunk;
+        const int t = min(tb + 4 * i + ld_key, ri.lk - 1);
+        const int64_t off = base + static_cast<int64_t>(t - tb) * a.c_ts;
+        // streaming (non-temporal) loads: every K/V byte is read exactly once, so keep it out of the caches' normal
+        // replacement; measured ~15% more bandwidth than default loads on MI355X for this stream
+        kq = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.kc + off));
+        vq = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vc + off));
+    };
+    auto load_chunk = [&](int c, u32x4 (&kr)[8], u32x4 (&vr)[8]) {
+        const int64_t base = chunk_base(c);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int t = min(tb + 4 * i + ld_key, ri.lk - 1);
-            const int64_t off = base + static_cast<int64_t>(in_page + (t - tb)) * a.c_ts;
-            // streaming (non-temporal) loads: every K/V byte is read exactly once, so keep it out of the caches'
-            // normal replacement; measured ~15% more bandwidth than default loads on MI355X for this stream
-            kr[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.kc + off));
-            vr[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vc + off));
-        }
+        for (int i = 0; i < 8; ++i) load_piece(c, base, i, kr[i], vr[i]);
     };
 
     // This wave's first kPrefetch chunks are requested before the query tile, so they are in flight together.
@@ -270,25 +282,39 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void attn_split_kernel(AttnArgs
     f32x16 o[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] = f32x16{};
-    // Registers -> the wave-private tiles. LDS executes one wave's accesses in issue order; the fences keep the
-    // compiler from moving these stores above the previous chunk's reads.
-    auto stage_chunk = [&](const u32x4 (&kr)[8], const u32x4 (&vr)[8]) {
-        compiler_fence();
+    // Registers -> the wave-private tiles, each register pair refilled with piece i of chunk cn (when cn < nch) as
+    // soon as it is stored, so the next chunk's loads leave while the rest is still being stored. LDS executes one
+    // wave's accesses in issue order; the fences keep the compiler from moving these stores above the previous
+    // chunk's reads.
+    auto stage_chunk = [&](u32x4 (&kr)[8], u32x4 (&vr)[8], int cn) {
+        if (cn < nch) {
+            const int64_t nbase = chunk_base(cn);
+            compiler_fence();
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int row = 4 * i + ld_key;
-            *reinterpret_cast<u32x4*>(ks + row * kRowStride + 8 * ld_piece) = kr[i];
-            *reinterpret_cast<u32x4*>(vs + row * kRowStride + 8 * ld_piece) = vr[i];
+            for (int i = 0; i < 8; ++i) {
+                const int row = 4 * i + ld_key;
+                *reinterpret_cast<u32x4*>(ks + row * kRowStride + 8 * ld_piece) = kr[i];
+                *reinterpret_cast<u32x4*>(vs + row * kRowStride + 8 * ld_piece) = vr[i];
+                load_piece(cn, nbase, i, kr[i], vr[i]);
+            }
+            compiler_fence();
+        } else {
+            compiler_fence();
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int row = 4 * i + ld_key;
+                *reinterpret_cast<u32x4*>(ks + row * kRowStride + 8 * ld_piece) = kr[i];
+                *reinterpret_cast<u32x4*>(vs + row * kRowStride + 8 * ld_piece) = vr[i];
+            }
+            compiler_fence();
         }
-        compiler_fence();
     };
 
-    // One chunk: stage it, request the chunk this wave does next, S^T = K Q^T, online softmax, O^T += V^T P^T.
+    // One chunk: stage it while requesting the chunk this wave does next, S^T = K Q^T, online softmax,
+    // O^T += V^T P^T.
     auto process_chunk = [&](int c, u32x4 (&kr)[8], u32x4 (&vr)[8]) {
         const int tb = k0 + c * kChunk;
-        stage_chunk(kr, vr);
-        const int cn = c + kWaves * kPrefetch;
-        if (cn < nch) load_chunk(cn, kr, vr);
+        stage_chunk(kr, vr, c + kWaves * kPrefetch);
 
         f32x16 acc = f32x16{};
 #pragma unroll

@@ -91,6 +91,19 @@ def test_sixty_two_splits_of_one_long_row(device):
     check(run_varlen(c, device, max_seqlen_k=32768), c)
 
 
+def test_units_longer_than_64_block_table_pages(device):
+    """32-key blocks. 34 rows of 2,080-2,608 keys (272 units: unsplit) span 65-82 pages per unit: the kernel holds
+    a unit's first 64 block ids in its lanes and reads the table for the pages past them. Two rows of 4,096 and
+    3,000 keys are split, so each split starts at a later page of its row's table."""
+    log_case("attention 32-key blocks: 34 unsplit rows of 65-82 pages; 2 split rows of 128 and 94 pages")
+    k_lens = [2080 + 16 * r for r in range(34)]
+    q_lens = [1 + (r % 4 == 0) for r in range(34)]
+    c = wl.verify_attention_case(q_lens, k_lens, 32, 8, 128, block_size=32)
+    check(run_varlen(c, device), c)
+    c = wl.verify_attention_case([8, 5], [4096, 3000], 32, 8, 128, block_size=32)
+    check(run_varlen(c, device), c)
+
+
 @pytest.mark.parametrize("seed", range(8))
 def test_random_shapes_across_split_plans(device, seed):
     """Seeded random batches (1-16 rows, 0-8 verify tokens, up to 4,000 keys, GQA groups 1/4/8) under graph-sized
