@@ -1364,13 +1364,14 @@ __device__ void markov_tail(const SelArgs& a, int64_t t, const char* row, float 
 // With one workgroup per sequence a batch of 64 leaves three quarters of the chip idle, so the split draw cuts each
 // row into segments of at most kSegKeys values, one workgroup each (8 at V = 151,936: 512 workgroups), in one
 // launch (markov_draw_kernel). Each workgroup keeps its segment's keys in registers, 40 per thread (the Markov
-// bias added and rounded to the logits' dtype, the temperature applied), and writes its top n_cand (key, index)
-// pairs in (value descending, index ascending) order: a first bound from ballots over the lanes' largest keys
-// leaves a short list of the keys at or above it (a few hundred), ranked exactly by comparing every pair with
-// every other; a list past kShortCap (massive ties) takes range histograms instead. The row's top n_cand are among
-// the union of its segments' top n_cand: the pairs go to the coherence point, each segment counts itself on the
-// row's counter, and the row's last segment to finish merges the lists (a pair's rank is its place in its own
-// list plus, per other list, the pairs above it) and finishes as markov_tail does: the top-k threshold and the
+// bias added and rounded to the logits' dtype, the temperature applied), and writes its keys at or above its own
+// rank-th largest (rank = the row's top-k window; ties included, at most n_cand) as (key, index) pairs in (value
+// descending, index ascending) order, with their count: a first bound from ballots over the lanes' largest keys
+// leaves a short list of the keys at or above it, ranked exactly by comparing every pair with every other; a list
+// past kShortCap (massive ties) takes range histograms instead. The row's candidates that can be kept are at or
+// above the row's rank-th largest, which is at least every segment's, so they are all in the union of the
+// segments' pairs. The pairs go to the coherence point, each segment counts itself on the row's counter, and the
+// row's last segment to finish merges the lists and finishes as markov_tail does: the top-k threshold and the
 // nucleus over the candidates (the same functions as probs_from_logits), Z, the race and the outputs.
 
 constexpr int kSegKeys = 19456;          // values of one segment (at most 40 per thread, kept in registers)
@@ -1393,6 +1394,7 @@ struct MarkovSplitArgs {
     int seg_len;                 // a multiple of 8
     int n_seg;
     uint64_t* pairs;             // [batch, n_seg, n_cand], written and read at the coherence point
+    int* seg_counts;             // [batch, n_seg] pairs each segment wrote (a prefix of its n_cand slots)
     int* counters;               // [batch] segments of the row finished; zero between calls
     const float* noise;
     int64_t noise_stride;
@@ -1425,20 +1427,41 @@ __device__ __forceinline__ float half_of(uint32_t w, int hi) {
     }
 }
 
-// The merge of a row's segment lists by the row's last segment to finish (markov_draw_kernel). The lists, each
-// sorted (value descending, index ascending, zeros of empty slots last), are read at the coherence point into the
-// upper half of the pair space, all loads issued before any is used. A tree of pairwise merges then keeps the top
-// n_cand of each pair of lists until one list is left (every pair is distinct: one index each). Then the top-k
-// threshold and the nucleus over those candidates, Z, the race and the outputs, as markov_tail does.
-// noise_c (this thread's candidate noise, C <= kSelThreads), tk and top_p were loaded before the row's count.
-__device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float noise_c, int64_t tk, float top_p,
-                                 SelShared& sh) {
+// How many of the first n pairs of buf (LDS, read by every lane at once) are greater than x: eight loads in flight
+// at a time rather than one round trip per pair.
+__device__ __forceinline__ int count_above(const uint64_t* buf, int n, uint64_t x) {
+    int above = 0;
+    int j = 0;
+    for (; j + 8 <= n; j += 8) {
+        uint64_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = buf[j + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) above += (v[u] > x) ? 1 : 0;
+    }
+    for (; j < n; ++j) above += (buf[j] > x) ? 1 : 0;
+    return above;
+}
+
+// The merge of a row's segment lists by the row's last segment to finish (markov_draw_kernel). Each list (sorted,
+// value descending, index ascending) and its count are read at the coherence point, all loads issued before any
+// is used. When the lists hold at most one pair per thread (the usual case: about the window's size per segment),
+// every pair is ranked against all the others at once; otherwise a tree of pairwise merges keeps the top n_cand of
+// each pair of lists until one is left. Every pair is distinct (one index each). Then the top-k threshold and the
+// nucleus over the candidates, Z, the race and the outputs, as markov_tail does: by wave 0 alone when the
+// candidates fit two per lane and the window 64, else by the workgroup.
+// noise_c and noise_c64 (the noise of candidates threadIdx.x and threadIdx.x + 64; C <= kSelThreads), tk and top_p
+// were loaded before the row's count.
+__device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float noise_c, float noise_c64, int64_t tk,
+                                 float top_p, SelShared& sh) {
     uint64_t* pairs = pair_buf(sh);
-    const int total = a.n_seg * a.n_cand;
     const int C = a.n_cand;
+    const int total = a.n_seg * C;
     const uint64_t* src = a.pairs + b * total;
     uint64_t* all = pairs + kPairCap / 2;
-    // every load issued before any is used: one round trip to the coherence point (total <= kPairCap / 2 pairs)
+    const int lane = lane_id();
+    // every load issued before any is used: one round trip to the coherence point (total <= kPairCap / 2 pairs,
+    // n_seg <= 64 counts, one per lane of every wave)
     constexpr int kPer = kPairCap / 2 / kSelThreads;
     uint64_t got[kPer];
 #pragma unroll
@@ -1446,59 +1469,168 @@ __device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float nois
         const int i = min(static_cast<int>(threadIdx.x) + r * kSelThreads, total - 1);
         got[r] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    int nz = 0;
+    const int cnt_raw = __hip_atomic_load(a.seg_counts + b * a.n_seg + min(lane, a.n_seg - 1), __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    const int cnt = lane < a.n_seg ? min(max(cnt_raw, 0), C) : 0;
+    const int cincl = wave_scan_incl_dpp(cnt);
+    const int n_all = __shfl(cincl, 63);   // pairs in all the lists
+    int real = min(C, n_all);
+    if (n_all <= kSelThreads) {
+        // The lists one after another (list s from the sum of the counts before it). Then every pair's rank: its
+        // place in its own list plus, in each other list, the number of pairs above it, by binary searches that
+        // advance eight lists at a time (one LDS round trip per halving for all eight).
 #pragma unroll
-    for (int r = 0; r < kPer; ++r) {
-        const int i = static_cast<int>(threadIdx.x) + r * kSelThreads;
-        if (i < total) {
-            all[i] = got[r];
-            nz += got[r] != 0ull ? 1 : 0;
-        }
-    }
-    nz = static_cast<int>(block_sum(static_cast<float>(nz), sh));   // its barriers publish `all`
-    const int want = min(C, nz);
-    // A tree of pairwise merges, each keeping the top C of its two lists: an element's rank in the merge is its
-    // place in its own list plus the number of the other list's pairs above it (a branch-free binary search). The
-    // nonzero pairs of two lists fill the first ranks, their zeros (empty slots) every rank after them, so every
-    // slot of the output is written. Lists 2m and 2m+1 merge into list m of the other half of the pair space;
-    // a last list without a mate is copied.
-    uint64_t* cur = all;
-    uint64_t* nxt = pairs;
-    for (int n_lists = a.n_seg; n_lists > 1; n_lists = (n_lists + 1) / 2) {
-        for (int e = threadIdx.x; e < n_lists * C; e += kSelThreads) {
+        for (int r = 0; r < kPer; ++r) {
+            const int e = static_cast<int>(threadIdx.x) + r * kSelThreads;
             const int li = e / C;
             const int i = e - li * C;
-            const uint64_t x = cur[e];
-            const int mate = li ^ 1;
-            int above = 0;
-            if (mate < n_lists) {
-                const uint64_t* other = cur + mate * C;
-                int lo = 0, hi = C;
-                for (int len = C; len > 0; len >>= 1) {   // floor(log2 C) + 1 halvings empty the interval
-                    const int mid = (lo + hi) >> 1;
-                    const bool open = lo < hi;
-                    const bool gt = other[min(mid, C - 1)] > x;
-                    lo = (open && gt) ? mid + 1 : lo;
-                    hi = (open && !gt) ? mid : hi;
+            const int c_li = __shfl(cnt, min(li, 63));
+            const int off = __shfl(cincl, min(li, 63)) - c_li;
+            if (e < total && i < c_li) all[off + i] = got[r];
+        }
+        int longest = cnt;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) longest = max(longest, __shfl_xor(longest, o));
+        __syncthreads();
+        const int t = static_cast<int>(threadIdx.x);
+        int own = 0;   // the list holding pair t: the number of lists that end at or before it
+        for (int l = 0; l < a.n_seg; ++l) own += (__builtin_amdgcn_readlane(cincl, l) <= t) ? 1 : 0;
+        const int own_start = __shfl(cincl, min(own, 63)) - __shfl(cnt, min(own, 63));
+        if (t < n_all) {
+            const uint64_t x = all[t];
+            int above = t - own_start;   // its place in its own list
+            for (int g0 = 0; g0 < a.n_seg; g0 += 8) {
+                int lo[8], hi[8], base[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int l = min(g0 + u, a.n_seg - 1);
+                    const int c_l = __builtin_amdgcn_readlane(cnt, l);
+                    base[u] = __builtin_amdgcn_readlane(cincl, l) - c_l;
+                    lo[u] = 0;
+                    hi[u] = (g0 + u < a.n_seg && g0 + u != own) ? c_l : 0;
                 }
-                above = lo;
+                for (int len = longest; len > 0; len >>= 1) {   // floor(log2 longest) + 1 halvings empty them
+                    uint64_t v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) v[u] = all[base[u] + min((lo[u] + hi[u]) >> 1, max(hi[u] - 1, 0))];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int mid = (lo[u] + hi[u]) >> 1;
+                        const bool open = lo[u] < hi[u];
+                        const bool gt = v[u] > x;
+                        lo[u] = (open && gt) ? mid + 1 : lo[u];
+                        hi[u] = (open && !gt) ? mid : hi[u];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) above += lo[u];
             }
-            const int rank = i + above;
-            if (rank < C) nxt[(li >> 1) * C + rank] = x;
+            if (above < C) pairs[above] = x;
         }
         __syncthreads();
-        uint64_t* t = cur;
-        cur = nxt;
-        nxt = t;
-    }
-    if (cur != pairs) {   // the top C of the union into the lower half (an odd number of levels leaves it above)
-        for (int i = threadIdx.x; i < C; i += kSelThreads) pairs[i] = cur[i];
+    } else {
+        // the lists at their slots, zero past each count (zeros sort below every pair)
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) {
+            const int e = static_cast<int>(threadIdx.x) + r * kSelThreads;
+            const int li = e / C;
+            const int i = e - li * C;
+            const int c_li = __shfl(cnt, min(li, 63));
+            if (e < total) all[e] = (i < c_li) ? got[r] : 0ull;
+        }
         __syncthreads();
+        // A tree of pairwise merges, each keeping the top C of its two lists: an element's rank in the merge is
+        // its place in its own list plus the number of the other list's pairs above it (a branch-free binary
+        // search). The nonzero pairs of two lists fill the first ranks, their zeros every rank after them, so every
+        // slot of the output is written. Lists 2m and 2m+1 merge into list m of the other half of the pair space;
+        // a last list without a mate is copied.
+        uint64_t* cur = all;
+        uint64_t* nxt = pairs;
+        for (int n_lists = a.n_seg; n_lists > 1; n_lists = (n_lists + 1) / 2) {
+            for (int e = threadIdx.x; e < n_lists * C; e += kSelThreads) {
+                const int li = e / C;
+                const int i = e - li * C;
+                const uint64_t x = cur[e];
+                const int mate = li ^ 1;
+                int above = 0;
+                if (mate < n_lists) {
+                    const uint64_t* other = cur + mate * C;
+                    int lo = 0, hi = C;
+                    for (int len = C; len > 0; len >>= 1) {   // floor(log2 C) + 1 halvings empty the interval
+                        const int mid = (lo + hi) >> 1;
+                        const bool open = lo < hi;
+                        const bool gt = other[min(mid, C - 1)] > x;
+                        lo = (open && gt) ? mid + 1 : lo;
+                        hi = (open && !gt) ? mid : hi;
+                    }
+                    above = lo;
+                }
+                const int rank = i + above;
+                if (rank < C) nxt[(li >> 1) * C + rank] = x;
+            }
+            __syncthreads();
+            uint64_t* t = cur;
+            cur = nxt;
+            nxt = t;
+        }
+        if (cur != pairs) {   // the top C of the union into the lower half (an odd number of levels leaves it above)
+            for (int i = threadIdx.x; i < C; i += kSelThreads) pairs[i] = cur[i];
+            __syncthreads();
+        }
     }
-    const int real = want;
     const int K = static_cast<int>(min(static_cast<int64_t>(a.max_top_k), a.vocab));
     int rank = static_cast<int>(min(tk > 0 ? tk : static_cast<int64_t>(K), static_cast<int64_t>(K)));
     rank = min(rank, real);
+    if (C <= 128 && rank <= 64) {
+        // Wave 0 alone, two candidates per lane (c = lane, lane + 64), with the workgroup path's arithmetic in the
+        // same order (Z: the sum over the first 64 candidates, then over the next 64), so the results are the same.
+        if (threadIdx.x >= 64) return;
+        const uint64_t p0 = lane < real ? pairs[lane] : 0ull;
+        const uint64_t p1 = lane + 64 < real ? pairs[lane + 64] : 0ull;
+        const uint32_t k0 = static_cast<uint32_t>(p0 >> 32);
+        const uint32_t k1 = static_cast<uint32_t>(p1 >> 32);
+        uint32_t theta_key = 0xffffffffu;   // no value: nothing kept
+        if (rank > 0) {
+            const uint32_t thr_key = static_cast<uint32_t>(pairs[rank - 1] >> 32);
+            float theta = nvs::key_float(thr_key);
+            if (a.has_top_p) theta = wave_top_p_threshold64(lane < rank ? k0 : 0u, rank, K, top_p, theta);
+            theta_key = nvs::float_key(theta);
+        }
+        // the kept candidates form a prefix of the sorted pairs
+        const int kept = __popcll(__ballot(lane < real && k0 >= theta_key)) +
+                         __popcll(__ballot(lane + 64 < real && k1 >= theta_key));
+        const float m = kept > 0 ? nvs::key_float(static_cast<uint32_t>(__shfl(static_cast<int>(k0), 0))) : 0.f;
+        const float e0 = lane < kept ? expf(nvs::key_float(k0) - m) : 0.f;
+        const float e1 = lane + 64 < kept ? expf(nvs::key_float(k1) - m) : 0.f;
+        const float z = wave_sum(e0) + wave_sum(e1);
+        uint64_t best = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int c = lane + 64 * h;
+            if (c >= C) continue;
+            const uint64_t pr = h ? p1 : p0;
+            float p = 0.f;
+            int32_t id = -1;
+            if (c < kept) {
+                p = expf(nvs::key_float(static_cast<uint32_t>(pr >> 32)) - m) / z;
+                id = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(pr));
+            }
+            a.cand_ids[b * a.cand_stride + c] = id;
+            a.cand_probs[b * a.cand_stride + c] = p;
+            const float score = p / (h ? noise_c64 : noise_c);
+            const uint64_t k64 = (static_cast<uint64_t>(nvs::float_key(score)) << 32) |
+                                 static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(c));
+            best = best > k64 ? best : k64;
+        }
+        best = wave_max_u64(best);
+        if (lane == 0) {
+            const float score = nvs::key_float(static_cast<uint32_t>(best >> 32));
+            const int win = (score > 0.f) ? static_cast<int>(0xffffffffu - static_cast<uint32_t>(best)) : 0;
+            a.draws[b * a.draws_stride] =
+                win < kept ? static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(pairs[win])) : int64_t{0};
+        }
+        return;
+    }
     uint32_t theta_key = 0xffffffffu;   // no value: nothing kept
     if (rank > 0) {
         const uint32_t thr_key = static_cast<uint32_t>(pairs[rank - 1] >> 32);
@@ -1545,7 +1677,7 @@ __device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float nois
 }
 
 template <int DT, bool VEC, bool BIAS>
-__global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplitArgs a) {
+__global__ __launch_bounds__(kSelThreads, 4) void markov_draw_kernel(MarkovSplitArgs a) {
 #pragma clang fp contract(off)
     // One SelShared, its members reused phase by phase: the segment's selection (histogram bins, bounds, the short
     // list in the pair space), then, in the row's last segment, the merge (pair space, sort buffer, reductions).
@@ -1557,6 +1689,8 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
     uint64_t* seg_pairs = reinterpret_cast<uint64_t*>(sh.sortbuf);   // the histogram path's want pairs, unsorted
     uint32_t* wbound = sh.wlo;
     uint32_t* whi = sh.wmax;
+    uint32_t& seg_theta = sh.sel_greater;   // the segment's want-th largest key
+    uint32_t& seg_count = sh.sel_equal;     // pairs the segment writes
     constexpr int W = piece_elems<DT>();
     const int seg = blockIdx.x;
     const int64_t b = blockIdx.y;
@@ -1564,6 +1698,7 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
     const int n = static_cast<int>(min(static_cast<int64_t>(a.seg_len), a.vocab - e_lo));
     const float temp = a.temps[b];
     const bool unit_temp = (temp == 1.f);
+    const int64_t row_tk = a.top_k[b];
     const int es = nvs::dtype_size(DT);
     const char* row = static_cast<const char*>(a.logits) + (b * a.row_stride + e_lo) * es;
     const char* brow = BIAS ? static_cast<const char*>(a.bias) + (b * a.bias_stride + e_lo) * es : nullptr;
@@ -1653,13 +1788,14 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
         }
     }
     __syncthreads();
-    // The want-th largest key. A lower bound first: each wave's ceil(want / 8)-th largest lane maximum (one ballot
-    // per bit), the smallest over the waves; every wave has that many lanes holding a key at or above it, so at
-    // least `want` keys are. Then histograms of the keys in [lo, lo + span], 256 bins spread over the range (keys
-    // of logits crowd into a few exponent values, so bins of fixed key digits would collide), each pass narrowing
-    // the range to the bin that holds the wanted rank, until a bin is one key.
-    const int want = min(a.n_cand, n);
-    const int rw = (want + kSelWaves - 1) / kSelWaves;   // <= 64: want <= kSplitMaxCand
+    // The segment's want-th largest key, want = the row's top-k window (a row without top-k: max_top_k) or the
+    // segment's length. A lower bound first: each wave's ceil(want / 8)-th largest lane maximum (one ballot per
+    // bit), the smallest over the waves; every wave has that many lanes holding a key at or above it, so at least
+    // `want` keys are.
+    const int K = static_cast<int>(min(static_cast<int64_t>(a.max_top_k), a.vocab));
+    const int want = static_cast<int>(min(min(row_tk > 0 ? row_tk : static_cast<int64_t>(K), static_cast<int64_t>(K)),
+                                          static_cast<int64_t>(n)));
+    const int rw = (want + kSelWaves - 1) / kSelWaves;   // <= 64: K <= n_cand <= kSplitMaxCand
     uint32_t wb = 0u;
 #pragma unroll
     for (int bit = 31; bit >= 0; --bit) {
@@ -1671,6 +1807,10 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
         wbound[threadIdx.x >> 6] = wb;
         whi[threadIdx.x >> 6] = wmaxk;
     }
+    if (threadIdx.x == 0) {
+        sh.count = 0;
+        seg_count = 0u;
+    }
     __syncthreads();
     uint32_t lo = 0xffffffffu, hi = 0u;
     for (int w = 0; w < kSelWaves; ++w) {
@@ -1680,13 +1820,11 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
     uint64_t* out = a.pairs + (b * a.n_seg + seg) * a.n_cand;
     // the segment's pairs go to the coherence point, where the row's merging workgroup (any XCD) reads them
     auto put = [&](int idx, uint64_t v) { __hip_atomic_store(out + idx, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-    // The short list: every key at or above the bound (at least want of them; a few hundred for logits of a few
-    // units' spread), appended wave by wave as (key, index) pairs to the pair space.
+    // The short list: every key at or above the bound (at least want of them), appended wave by wave as
+    // (key, index) pairs to the pair space: each lane's count, one prefix over the wave and one reservation per
+    // wave, then the lane's keys in order.
     uint64_t* list = pair_buf(sh);
-    if (threadIdx.x == 0) sh.count = 0;
-    __syncthreads();
-    if (want > 0) {
-        // each lane's count, one prefix over the wave and one reservation per wave, then the lane's keys in order
+    {
         int mine = 0;
 #pragma unroll
         for (int q = 0; q < kMaxPc * W; ++q) mine += (q < qlim && kr[q] >= lo) ? 1 : 0;
@@ -1708,19 +1846,41 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
     __syncthreads();
     const int nl = sh.count;
     if (nl <= kShortCap) {
-        // every pair's rank in the list (all pairs differ: one index each); the first want are the segment's
-        for (int p = threadIdx.x; p < nl; p += kSelThreads) {
-            const uint64_t v = list[p];
-            int above = 0;
-            for (int j = 0; j < nl; ++j) above += (list[j] > v) ? 1 : 0;
-            if (above < want) put(above, v);
+        // Every pair's rank in the list (all pairs differ: one index each). The pair ranked want - 1 holds the
+        // segment's want-th largest key; every pair at or above that key (the ties after it included) goes to its
+        // rank, up to n_cand of them.
+        uint64_t pv[kShortCap / kSelThreads];
+        int pa[kShortCap / kSelThreads];
+#pragma unroll
+        for (int r = 0; r < kShortCap / kSelThreads; ++r) {
+            const int p = static_cast<int>(threadIdx.x) + r * kSelThreads;
+            pv[r] = 0ull;
+            pa[r] = kShortCap;
+            if (p < nl) {
+                const uint64_t v = list[p];
+                const int above = count_above(list, nl, v);
+                pv[r] = v;
+                pa[r] = above;
+                if (above == want - 1) seg_theta = static_cast<uint32_t>(v >> 32);
+            }
         }
+        __syncthreads();
+        const uint32_t th = seg_theta;
+        uint32_t mine = 0u;
+#pragma unroll
+        for (int r = 0; r < kShortCap / kSelThreads; ++r) {
+            if (pa[r] < a.n_cand && static_cast<uint32_t>(pv[r] >> 32) >= th) {
+                put(pa[r], pv[r]);
+                ++mine;
+            }
+        }
+        if (mine > 0u) atomicAdd(&seg_count, mine);
     } else {
     // Massive ties at the bound: range histograms find the want-th largest key, the keys above it are taken, then
-    // the ties at it in index order.
+    // the ties at it in index order, up to n_cand pairs in all.
     uint32_t span = hi - lo;
     uint32_t rank = static_cast<uint32_t>(want);
-    for (int pass = 0; pass < 5 && want > 0; ++pass) {
+    for (int pass = 0; pass < 5; ++pass) {
         const int shift = span < 256u ? 0 : 24 - __clz(span);   // (span >> shift) < 256
         if (threadIdx.x < 256) hist[threadIdx.x] = 0u;
         __syncthreads();
@@ -1744,9 +1904,8 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
         if (shift == 0) break;
         span = (1u << shift) - 1u;
     }
-    const uint32_t prefix = lo;
-    const uint32_t t_key = prefix;
-    // The keys above the threshold (fewer than want) in any order, then the first want - n_gt ties in index
+    const uint32_t t_key = lo;
+    // The keys above the threshold (fewer than want) in any order, then the first n_cand - n_gt ties in index
     // order. Ties of each register group are counted per thread, and one workgroup prefix over all groups at once
     // gives every tie its rank.
     if (threadIdx.x == 0) n_gt = 0;
@@ -1755,7 +1914,7 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
     for (int j = 0; j < kMaxPc; ++j) {
         cnt[j] = 0;
 #pragma unroll
-        for (int c = 0; c < W; ++c) cnt[j] += (j * W + c < qlim && want > 0 && kr[j * W + c] == t_key) ? 1 : 0;
+        for (int c = 0; c < W; ++c) cnt[j] += (j * W + c < qlim && kr[j * W + c] == t_key) ? 1 : 0;
     }
     int incl[kMaxPc];
 #pragma unroll
@@ -1768,7 +1927,7 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
 #pragma unroll
     for (int q = 0; q < kMaxPc * W; ++q) {
         const uint32_t k = kr[q];
-        if (q < qlim && want > 0 && k > t_key) {
+        if (q < qlim && k > t_key) {
             const int i = (static_cast<int>(threadIdx.x) + (q / W) * kSelThreads) * W + q % W;
             seg_pairs[atomicAdd(&n_gt, 1)] = (static_cast<uint64_t>(k) << 32) |
                                              (0xffffffffu - static_cast<uint32_t>(e_lo + i));
@@ -1776,7 +1935,7 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
     }
     __syncthreads();
     const int gt = n_gt;
-    const int need = want - gt;
+    const int need = a.n_cand - gt;
     const int wave = static_cast<int>(threadIdx.x >> 6);
     int base = 0;   // ties of earlier groups, every thread
 #pragma unroll
@@ -1791,7 +1950,7 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
 #pragma unroll
         for (int c = 0; c < W; ++c) {
             const int q = j * W + c;
-            if (q < qlim && want > 0 && kr[q] == t_key) {
+            if (q < qlim && kr[q] == t_key) {
                 if (r < need) {
                     const int i = (static_cast<int>(threadIdx.x) + j * kSelThreads) * W + c;
                     seg_pairs[gt + r] = (static_cast<uint64_t>(t_key) << 32) |
@@ -1802,24 +1961,26 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
         }
         base += total_j;
     }
-    // the segment's list, sorted: each pair goes to its rank among the want pairs (all distinct)
+    // the segment's pairs, sorted: each pair goes to its rank among them (all distinct)
+    const int n_out = gt + min(base, need);
     __syncthreads();
-    for (int p = threadIdx.x; p < want; p += kSelThreads) {
+    for (int p = threadIdx.x; p < n_out; p += kSelThreads) {
         const uint64_t v = seg_pairs[p];
-        int above = 0;
-        for (int q = 0; q < want; ++q) above += (seg_pairs[q] > v) ? 1 : 0;
-        put(above, v);
+        put(count_above(seg_pairs, n_out, v), v);
     }
+    if (threadIdx.x == 0) seg_count = static_cast<uint32_t>(n_out);
     }
-    // empty slots (a segment with fewer values than candidates) hold 0, below every pair
-    for (int p = want + threadIdx.x; p < a.n_cand; p += kSelThreads) put(p, 0ull);
 
-    // What the merge needs besides the lists, requested now so it arrives during the count's round trip.
+    // What the merge needs besides the lists.
     const float noise_c = threadIdx.x < a.n_cand ? a.noise[b * a.noise_stride + threadIdx.x] : 1.f;
-    const int64_t row_tk = a.top_k[b];
+    const float noise_c64 = threadIdx.x + 64 < a.n_cand ? a.noise[b * a.noise_stride + threadIdx.x + 64] : 1.f;
     const float row_top_p = a.has_top_p ? a.top_p[b] : 1.f;
-    // Count the segment on the row's counter once every wave's stores have completed; the row's last segment to
-    // count merges. Its loads are issued after its own count returned, at the coherence point.
+    // Count the segment on the row's counter once every wave's stores (and thread 0's count) have completed; the
+    // row's last segment to count merges. Its loads are issued after its own count returned, at the coherence point.
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.seg_counts + b * a.n_seg + seg, static_cast<int>(seg_count), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -1829,7 +1990,7 @@ __global__ __launch_bounds__(kSelThreads, 2) void markov_draw_kernel(MarkovSplit
     __syncthreads();
     if (!sh.last) return;
     if (threadIdx.x == 0) __hip_atomic_store(a.counters + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    markov_merge_row(a, b, noise_c, row_tk, row_top_p, sh);
+    markov_merge_row(a, b, noise_c, noise_c64, row_tk, row_top_p, sh);
 }
 
 
@@ -2939,7 +3100,9 @@ static void markov_segments(int64_t vocab, int* n_seg, int* seg_len) {
 static bool markov_split(int64_t vocab, int num_candidates) {
     int n_seg, seg_len;
     markov_segments(vocab, &n_seg, &seg_len);
-    return num_candidates <= kSplitMaxCand && static_cast<int64_t>(n_seg) * num_candidates <= kPairCap / 2;
+    // the merge keeps the row's lists in half the pair space and the segments' counts in the lanes of a wave
+    return num_candidates <= kSplitMaxCand && n_seg <= 64 &&
+           static_cast<int64_t>(n_seg) * num_candidates <= kPairCap / 2;
 }
 
 template <int DT>
@@ -2962,8 +3125,9 @@ extern "C" int nvs_markov_draw_workspace_size(int64_t batch, int64_t vocab, int 
               "markov_draw_workspace_size: bad arguments");
     int n_seg, seg_len;
     markov_segments(vocab, &n_seg, &seg_len);
+    // the segments' pairs [batch, n_seg, n_cand] u64, then their counts [batch, n_seg] int32
     *bytes = markov_split(vocab, num_candidates)
-                 ? static_cast<size_t>(batch) * n_seg * num_candidates * sizeof(uint64_t) : 0;
+                 ? static_cast<size_t>(batch) * n_seg * (num_candidates * sizeof(uint64_t) + sizeof(int32_t)) : 0;
     return NVS_OK;
 }
 
@@ -2999,7 +3163,8 @@ extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t log
     if (markov_split(vocab, num_candidates)) {
         MarkovSplitArgs m{};
         markov_segments(vocab, &m.n_seg, &m.seg_len);
-        const size_t need = static_cast<size_t>(batch) * m.n_seg * num_candidates * sizeof(uint64_t);
+        const size_t pair_bytes = static_cast<size_t>(batch) * m.n_seg * num_candidates * sizeof(uint64_t);
+        const size_t need = pair_bytes + static_cast<size_t>(batch) * m.n_seg * sizeof(int32_t);
         NVS_CHECK(workspace != nullptr && workspace_bytes >= need, NVS_ERR_WORKSPACE,
                   "markov_draw: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
         NVS_CHECK(row_counters != nullptr, NVS_ERR_INVALID,
@@ -3018,6 +3183,7 @@ extern "C" int nvs_markov_draw(const void* logits, int logits_dtype, int64_t log
         m.has_top_p = has_top_p;
         m.n_cand = num_candidates;
         m.pairs = static_cast<uint64_t*>(workspace);
+        m.seg_counts = reinterpret_cast<int*>(static_cast<unsigned char*>(workspace) + pair_bytes);
         m.noise = noise;
         m.noise_stride = noise_row_stride;
         m.cand_ids = cand_ids;
