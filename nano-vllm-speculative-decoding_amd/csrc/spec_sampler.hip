@@ -2312,16 +2312,25 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             }
         }
         lcnt = min(lcnt, kLaneCap);   // past it only when the row goes to the exact path
+        // The lane's list in registers, read in one LDS round trip (slots past lcnt are never used): the loops
+        // below over the list would otherwise wait for one LDS read per slot.
+        uint32_t lk[kLaneCap];
+#pragma unroll
+        for (int s = 0; s < kLaneCap; ++s) lk[s] = wkey[s * 64 + lane];
         if (raw_mode) {
             // the lists, the bound and the largest key move to scaled values: one division per listed value
-            for (int s = 0; s < lcnt; ++s)
-                wkey[s * 64 + lane] = nvs::float_key(nvs::key_float(wkey[s * 64 + lane]) / temp);
+#pragma unroll
+            for (int s = 0; s < kLaneCap; ++s) {
+                if (s < lcnt) {
+                    lk[s] = nvs::float_key(nvs::key_float(lk[s]) / temp);
+                    wkey[s * 64 + lane] = lk[s];
+                }
+            }
             tau_key = tau_key == 0u ? 0u : nvs::float_key(nvs::key_float(tau_key) / temp);
             hmax = hmax == 0u ? 0u : nvs::float_key(nvs::key_float(hmax) / temp);
         }
         const uint32_t wave_hi = wave_max_u32(hmax);
         const int wave_total = wave_sum_i32(lcnt);
-        const int max_cnt = static_cast<int>(wave_max_u32(static_cast<uint32_t>(lcnt)));
         if (lane == 0) {
             sh.wcount[wave] = wave_total;
             if (overflow) sh.overflow = 1;
@@ -2356,12 +2365,9 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             }
             const uint32_t range = hi - lo;
             shift = range < 256u ? 0 : 24 - __clz(range);
-            for (int s = 0; s < max_cnt; ++s) {
-                if (s < lcnt) {
-                    const uint32_t key = wkey[s * 64 + lane];
-                    if (key >= lo) atomicAdd(&sh.hist[(key - lo) >> shift], 1u);
-                }
-            }
+#pragma unroll
+            for (int s = 0; s < kLaneCap; ++s)
+                if (s < lcnt && lk[s] >= lo) atomicAdd(&sh.hist[(lk[s] - lo) >> shift], 1u);
             __syncthreads();
             wave_pick_bin(sh.hist, static_cast<uint32_t>(rank), bin, bin_rank);
             // the same on every wave; a histogram with fewer than rank keys (never expected) goes to the exact path
@@ -2370,29 +2376,36 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             exact = !picked;
             fast = picked && n_top <= kTopCap;
             if (fast) {
-                const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-                for (int s = 0; s < max_cnt; ++s) {
-                    const int i = s * 64 + lane;
-                    const uint32_t key = s < lcnt ? wkey[i] : 0u;
+                // each lane's entries in the picked bin or above it (and in the bin), one prefix over the wave and
+                // one reservation per wave and list, then the lane's entries in order
+                int n_take = 0, n_bin = 0;
+#pragma unroll
+                for (int s = 0; s < kLaneCap; ++s) {
+                    const bool in = s < lcnt && lk[s] >= lo;
+                    const uint32_t d = (lk[s] - lo) >> shift;
+                    n_take += (in && d >= bin) ? 1 : 0;
+                    n_bin += (in && d == bin) ? 1 : 0;
+                }
+                const int incl_t = wave_scan_incl_dpp(n_take);
+                const int incl_b = wave_scan_incl_dpp(n_bin);
+                int base_t = 0, base_b = 0;
+                if (lane == 63) {
+                    if (incl_t > 0) base_t = atomicAdd(&sh.count, incl_t);
+                    if (incl_b > 0) base_b = atomicAdd(&sh.bin_count, incl_b);
+                }
+                int pt = __shfl(base_t, 63) + incl_t - n_take;
+                int pb = __shfl(base_b, 63) + incl_b - n_bin;
+#pragma unroll
+                for (int s = 0; s < kLaneCap; ++s) {
+                    const uint32_t key = lk[s];
                     const bool in = s < lcnt && key >= lo;
                     const uint32_t d = (key - lo) >> shift;
-                    const bool take = in && d >= bin;
-                    const uint64_t bal = __ballot(take);
-                    if (bal == 0ull) continue;
-                    int base = 0;
-                    if (lane == 0) base = atomicAdd(&sh.count, __popcll(bal));
-                    base = __shfl(base, 0);
-                    const bool at_bin = take && d == bin;
-                    const uint64_t bbal = __ballot(at_bin);
-                    int bbase = 0;
-                    if (lane == 0 && bbal != 0ull) bbase = atomicAdd(&sh.bin_count, __popcll(bbal));
-                    bbase = __shfl(bbase, 0);
-                    if (take) {
-                        const int p = base + __popcll(bal & below);
-                        sh.sortbuf[p] = key;
-                        sh.sortbuf[kTopCap + p] = static_cast<uint32_t>(widx[i]);
+                    if (in && d >= bin) {
+                        sh.sortbuf[pt] = key;
+                        sh.sortbuf[kTopCap + pt] = static_cast<uint32_t>(widx[s * 64 + lane]);
+                        ++pt;
+                        if (d == bin) bin_keys[pb++] = key;
                     }
-                    if (at_bin) bin_keys[bbase + __popcll(bbal & below)] = key;
                 }
             }
             __syncthreads();
@@ -2401,6 +2414,15 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
             // Wave 0 finishes the row alone: the threshold, the softmax sum over the kept keys and, for the fused
             // accept, this position's accept test, its race and its record.
             if (wave == 0) {
+                const int n_top = sh.count;
+                uint32_t kk[kSelWaves];
+                int32_t ki[kSelWaves];
+#pragma unroll
+                for (int w = 0; w < kSelWaves; ++w) {
+                    const int c = w * 64 + lane;
+                    kk[w] = c < n_top ? sh.sortbuf[c] : 0u;
+                    ki[w] = c < n_top ? static_cast<int32_t>(sh.sortbuf[kTopCap + c]) : 0;
+                }
                 // threshold: the largest key of the bin with at least bin_rank keys of the bin at or above it
                 const int nb_keys = sh.bin_count;
                 uint32_t cand = 0u;
@@ -2413,15 +2435,6 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                 const uint32_t thr_key = wave_max_u32(cand);
                 const float m = nvs::key_float(hi);
                 const float mu_f = (m == -INFINITY) ? 0.f : m;
-                const int n_top = sh.count;
-                uint32_t kk[kSelWaves];
-                int32_t ki[kSelWaves];
-#pragma unroll
-                for (int w = 0; w < kSelWaves; ++w) {
-                    const int c = w * 64 + lane;
-                    kk[w] = c < n_top ? sh.sortbuf[c] : 0u;
-                    ki[w] = c < n_top ? static_cast<int32_t>(sh.sortbuf[kTopCap + c]) : 0;
-                }
                 uint32_t theta_key = thr_key;
                 if (a.has_top_p) {
                     // top-p over the rank candidates (rank <= 64): the keys above the threshold (fewer than rank)
