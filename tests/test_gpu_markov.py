@@ -95,6 +95,23 @@ def test_random_rows_match_the_oracle(device, vocab, dtype, batch):
     check_candidates(q, want, "random rows")
 
 
+@pytest.mark.parametrize("vocab, dtype, top_k", [
+    (151936, torch.bfloat16, [100, 200, 64, 150]),   # 264 candidates, windows past 64: the workgroup finish
+    (200000, torch.float32, [20, 5, 50, 1]),         # 11 segments: the merge's searches in two groups of lists
+])
+def test_wide_windows_and_many_segments_match_the_oracle(device, vocab, dtype, top_k):
+    log_case(f"markov rows: V={vocab} {dtype} top_k={top_k}")
+    g = torch.Generator().manual_seed(vocab + top_k[0])
+    batch = 8
+    logits = (torch.randn(batch, 3, vocab, generator=g) * 3).to(dtype)
+    table = (torch.randn(16, vocab, generator=g) * 2).to(dtype)
+    st = sampling(device, [1.0, 0.7, 1.3, 1.0] * 2, top_k * 2, [1.0, 0.8, 0.95, 1.0] * 2)
+    anchors = torch.randint(0, vocab, (batch,), generator=g)
+    drafts, q, want = run_both(device, logits, anchors, table, st, seed=3)
+    assert torch.equal(drafts, want[0]), f"drafts differ at {(drafts != want[0]).nonzero()[:5].tolist()}"
+    check_candidates(q, want, "wide windows / many segments")
+
+
 @pytest.mark.parametrize("ties", [5000, 20000])
 def test_ties_beyond_the_candidates(device, ties):
     # ten distinct top values, then `ties` copies of the 11th; top-k 11 keeps them all, the candidates keep the
