@@ -33,6 +33,7 @@ METRIC = "verify-attn µs/layer & HBM GB/s (% of 8 TB/s) at B=64, 8 q, 3k ctx"
 MEASURED_TRAFFIC = {
     "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200": 789_697_414,              # head-major caches, 00f9586
     "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_token_major": 789_711_469,  # 00f9586
+    "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_kv_interleaved": 789_713_053,  # 47810ec
     "spec_accept_b64_k7_v151936_fp32_topk64": 320_116_159,                              # 00f9586
     "markov_draw_b64_v151936_bf16_rank64": 40_264_806,                                  # 00f9586
 }
@@ -101,11 +102,15 @@ def attention_bench(args, dev):
     kv, qo = case.kv_bytes(), case.qo_bytes()
     flops = case.flops()
     ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
-    # The reference's token-major layout (model_runner.py:160), then the library's head-major layout (each
-    # (block, kv head) one contiguous run): the same values through the same kernel.
+    # The reference's token-major layout (model_runner.py:160), the library's head-major layout (each (block, kv
+    # head) one contiguous run in K and one in V), then K and V interleaved (each (block, kv head)'s keys and then
+    # values one run): the same values through the same kernel.
     timed = {}
-    for layout in ("token_major", "head_major"):
-        g = (case.head_major() if layout == "head_major" else case).to(dev)
+    for layout in ("token_major", "head_major", "kv_interleaved"):
+        if layout == "kv_interleaved":
+            g = case.kv_interleaved(dev)
+        else:
+            g = (case.head_major() if layout == "head_major" else case).to(dev)
         out = torch.empty_like(g.q)
 
         def step():
@@ -120,12 +125,14 @@ def attention_bench(args, dev):
         hip_out = out.float().cpu()   # the last timed launch's output (both layouts give the same bits)
         del g, out
     ms, gbs = timed["head_major"]
-    tm_ms, tm_gbs = timed["token_major"]
-    token_major = {"workload": "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200",
-                   "kv_layout": "token_major [blocks, 256, 8, 128] (the reference's)", "us": round(tm_ms * 1e3, 2),
-                   "GBs": round(tm_gbs, 1), "frac": round(tm_gbs / HBM_PEAK_GBS, 4),
-                   "traffic": MEASURED_TRAFFIC["verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_token_major"]}
-    return case, ms, kv + qo, gbs, flops, token_major, hip_out
+    layouts = {}
+    for layout, desc in (("token_major", "token_major [blocks, 256, 8, 128] (the reference's)"),
+                         ("kv_interleaved", "kv_interleaved: K and V views of [blocks, 8, 2, 256, 128] memory")):
+        l_ms, l_gbs = timed[layout]
+        layouts[layout] = {"workload": "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200", "kv_layout": desc,
+                           "us": round(l_ms * 1e3, 2), "GBs": round(l_gbs, 1), "frac": round(l_gbs / HBM_PEAK_GBS, 4),
+                           "traffic": MEASURED_TRAFFIC[f"verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_{layout}"]}
+    return case, ms, kv + qo, gbs, flops, layouts, hip_out
 
 
 def launch_bound_bench(args, dev):
@@ -700,8 +707,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
 
-    case, ms, nbytes, gbs, flops, token_major, hip_out = attention_bench(args, dev)
-    extra = {"attention_token_major": token_major, "c2": launch_bound_bench(args, dev),
+    case, ms, nbytes, gbs, flops, layouts, hip_out = attention_bench(args, dev)
+    extra = {"attention_token_major": layouts["token_major"], "attention_kv_interleaved": layouts["kv_interleaved"],
+             "c2": launch_bound_bench(args, dev),
              "draft_block": draft_block_bench(args, dev),
              "qk_norm_rope_store": qk_rope_bench(args, dev)}
     if args.sampler == "on":

@@ -72,12 +72,36 @@ class AttentionCase:
         fields["v_cache"] = head_major(self.v_cache)
         return AttentionCase(**fields)
 
+    def kv_interleaved(self, device=None) -> "AttentionCase":
+        """The same case on `device` with both caches interleaved (kv_cache_empty). Built on the device directly:
+        .to() would not keep the caches' strides."""
+        fields = {name: getattr(self, name) for name in self.__dataclass_fields__}
+        for name, value in fields.items():
+            if isinstance(value, torch.Tensor):
+                fields[name] = value.to(device)
+        k, v = kv_cache_empty(*self.k_cache.shape, dtype=self.k_cache.dtype, device=device)
+        k.copy_(self.k_cache)
+        v.copy_(self.v_cache)
+        fields["k_cache"], fields["v_cache"] = k, v
+        return AttentionCase(**fields)
+
 
 def head_major_empty(*shape: int, dtype: torch.dtype, device=None) -> torch.Tensor:
     """An uninitialised cache [..., blocks, block_size, Hkv, D] whose memory is [..., blocks, Hkv, block_size, D]:
     every (block, kv head) is one contiguous run of block_size * D elements."""
     *lead, block_size, hkv, d = shape
     return torch.empty(*lead, hkv, block_size, d, dtype=dtype, device=device).transpose(-3, -2)
+
+
+def kv_cache_empty(*shape: int, dtype: torch.dtype, device=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Uninitialised K and V caches, each [..., blocks, block_size, Hkv, D], interleaved: the memory is [..., blocks,
+    Hkv, 2, block_size, D], so every (block, kv head) holds its block_size keys and then their values as one
+    contiguous run. The kernels read and write it through its strides like any other layout; on the batch-64 verify
+    layer it measured within about 1% of separate head-major caches (faster in variant sweeps, not in the bench's
+    fixed order)."""
+    *lead, block_size, hkv, d = shape
+    buf = torch.empty(*lead, hkv, 2, block_size, d, dtype=dtype, device=device)
+    return buf.select(-3, 0).transpose(-3, -2), buf.select(-3, 1).transpose(-3, -2)
 
 
 def head_major(cache: torch.Tensor) -> torch.Tensor:

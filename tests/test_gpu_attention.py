@@ -292,7 +292,7 @@ def test_store_kvcache_bit_exact_strided_value_and_padding(device):
     assert torch.equal(gk.cpu(), want_k) and torch.equal(gv.cpu(), want_v)
 
 
-@pytest.mark.parametrize("layout", ["token_major", "head_major"])
+@pytest.mark.parametrize("layout", ["token_major", "head_major", "kv_interleaved"])
 @pytest.mark.parametrize("dtype, head_dim", [(torch.float32, 64), (torch.float16, 128), (torch.bfloat16, 4)])
 def test_store_kvcache_other_dtypes_and_unaligned_rows(device, dtype, head_dim, layout):
     log_case(f"store_kvcache {dtype} head_dim {head_dim} {layout}")
@@ -306,6 +306,10 @@ def test_store_kvcache_other_dtypes_and_unaligned_rows(device, dtype, head_dim, 
     if layout == "head_major":
         gk = wl.head_major_empty(*want_k.shape, dtype=dtype, device=device).zero_()
         gv = wl.head_major_empty(*want_v.shape, dtype=dtype, device=device).zero_()
+    elif layout == "kv_interleaved":
+        gk, gv = wl.kv_cache_empty(*want_k.shape, dtype=dtype, device=device)
+        gk.zero_()
+        gv.zero_()
     else:
         gk, gv = torch.zeros_like(want_k, device=device), torch.zeros_like(want_v, device=device)
     nattn.store_kvcache(key.to(device), value.to(device), gk, gv, slots.to(device))
@@ -334,16 +338,21 @@ def test_store_kvcache_head_major_strided_value(device):
     assert torch.equal(gk.cpu(), want_k) and torch.equal(gv.cpu(), want_v)
 
 
+@pytest.mark.parametrize("layout", ["head_major", "kv_interleaved"])
 @pytest.mark.parametrize("shape", ["c2_split", "c3", "draft_block"])
-def test_head_major_cache_gives_the_token_major_result(device, shape):
-    """The kernel reads a cache through its strides: head-major memory gives bit for bit the token-major result."""
-    log_case(f"attention head-major vs token-major {shape}")
+def test_head_major_cache_gives_the_token_major_result(device, shape, layout):
+    """The kernel reads a cache through its strides: head-major memory, and K and V interleaved in one buffer (each
+    block and kv head's keys and then values one run), give bit for bit the token-major result."""
+    log_case(f"attention {layout} vs token-major {shape}")
     if shape == "draft_block":
         c = wl.verify_attention_case([7] * 16, [900 + 37 * i for i in range(16)], 32, 8, 128, pad_tokens_to=1)
     else:
         c = wl.config_c2() if shape == "c2_split" else wl.config_c3()
-    g, h = c.to(device), c.head_major().to(device)
-    assert h.k_cache.stride(1) == 128 and torch.equal(h.k_cache, g.k_cache)
+    g = c.to(device)
+    h = c.head_major().to(device) if layout == "head_major" else c.kv_interleaved(device)
+    assert h.k_cache.stride(1) == 128 and torch.equal(h.k_cache, g.k_cache) and torch.equal(h.v_cache, g.v_cache)
+    if layout == "kv_interleaved":
+        assert h.v_cache.data_ptr() - h.k_cache.data_ptr() == 256 * 128 * h.k_cache.element_size()
     if shape == "draft_block":
         ctx = torch.tensor(c.k_lens, dtype=torch.int32, device=device)
         outs = [nattn._paged_attention(x.q, x.k_cache, x.v_cache, x.block_tables, None, None, ctx, 7, 16, 7, 4096,

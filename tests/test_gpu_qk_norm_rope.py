@@ -42,11 +42,16 @@ def close_to_oracle(got: torch.Tensor, want: torch.Tensor, what: str, rotated: t
     assert same >= 0.99, f"{what}: only {100 * same:.2f}% bit-identical"
 
 
-def run_case(case: wl.QkRopeCase, device, keys_only=False, norms=True, in_place=False, head_major=False):
+def run_case(case: wl.QkRopeCase, device, keys_only=False, norms=True, in_place=False, head_major=False,
+             kv_interleaved=False):
     g = case.to(device)
     q, k, v = g.split()
     if head_major:
         kc, vc = wl.head_major(g.k_cache), wl.head_major(g.v_cache)
+    elif kv_interleaved:
+        kc, vc = wl.kv_cache_empty(*g.k_cache.shape, dtype=g.k_cache.dtype, device=device)
+        kc.copy_(g.k_cache)
+        vc.copy_(g.v_cache)
     else:
         kc, vc = g.k_cache.clone(), g.v_cache.clone()
     qw = g.q_norm_weight if norms else None
@@ -97,6 +102,17 @@ def test_head_major_cache(device):
     case = wl.qk_rope_case(296, num_padding=8, seed=6)
     out, kc, vc, q_ref, refs, q_norm = run_case(case, device, head_major=True)
     assert kc.stride(1) == case.head_dim and not kc.is_contiguous()
+    close_to_oracle(out, q_ref, "q", q_norm)
+    check_caches(case, kc, vc, refs)
+
+
+def test_kv_interleaved_cache(device):
+    """K and V interleaved in one buffer (each block and kv head's keys, then its values, one contiguous run): the
+    same values land in the same logical slots, and nothing else is written."""
+    log_case("qk norm rope store into kv-interleaved caches, qwen3-8b T=296")
+    case = wl.qk_rope_case(296, num_padding=8, seed=7)
+    out, kc, vc, q_ref, refs, q_norm = run_case(case, device, kv_interleaved=True)
+    assert kc.stride(2) == 2 * kc.shape[1] * case.head_dim and not kc.is_contiguous()
     close_to_oracle(out, q_ref, "q", q_norm)
     check_caches(case, kc, vc, refs)
 
