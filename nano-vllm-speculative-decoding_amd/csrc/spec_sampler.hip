@@ -1699,6 +1699,11 @@ __global__ __launch_bounds__(kSelThreads, 4) void markov_draw_kernel(MarkovSplit
     const float temp = a.temps[b];
     const bool unit_temp = (temp == 1.f);
     const int64_t row_tk = a.top_k[b];
+    // What the merge needs besides the lists, requested first (before the segment's keys, which then cannot delay
+    // them): used only by the row's last segment.
+    const float noise_c = threadIdx.x < a.n_cand ? a.noise[b * a.noise_stride + threadIdx.x] : 1.f;
+    const float noise_c64 = threadIdx.x + 64 < a.n_cand ? a.noise[b * a.noise_stride + threadIdx.x + 64] : 1.f;
+    const float row_top_p = a.has_top_p ? a.top_p[b] : 1.f;
     const int es = nvs::dtype_size(DT);
     const char* row = static_cast<const char*>(a.logits) + (b * a.row_stride + e_lo) * es;
     const char* brow = BIAS ? static_cast<const char*>(a.bias) + (b * a.bias_stride + e_lo) * es : nullptr;
@@ -1971,10 +1976,6 @@ __global__ __launch_bounds__(kSelThreads, 4) void markov_draw_kernel(MarkovSplit
     if (threadIdx.x == 0) seg_count = static_cast<uint32_t>(n_out);
     }
 
-    // What the merge needs besides the lists.
-    const float noise_c = threadIdx.x < a.n_cand ? a.noise[b * a.noise_stride + threadIdx.x] : 1.f;
-    const float noise_c64 = threadIdx.x + 64 < a.n_cand ? a.noise[b * a.noise_stride + threadIdx.x + 64] : 1.f;
-    const float row_top_p = a.has_top_p ? a.top_p[b] : 1.f;
     // Count the segment on the row's counter once every wave's stores (and thread 0's count) have completed; the
     // row's last segment to count merges. Its loads are issued after its own count returned, at the coherence point.
     __syncthreads();
