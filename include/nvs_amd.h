@@ -272,10 +272,11 @@ int nvs_spec_accept_noalloc(const void* logits, int logits_dtype, int64_t logits
  * top-k (the reference's candidate rows require it; a row with top_k <= 0 is drawn among its top max_top_k).
  * logits and bias [batch, vocab] fp32 / bf16 / fp16 (one dtype) with row strides; noise [batch, >= num_candidates]
  * fp32, the row's exponential noise by candidate rank; parameters per row as in nvs_probs_from_logits.
- * min(max_top_k, vocab) <= num_candidates <= 7168; batch <= 65535. Up to 512 candidates the row is cut into
- * segments drawn by separate workgroups of one launch, and the row's last segment to finish merges them
+ * min(max_top_k, vocab) <= num_candidates <= 7168; batch <= 65535. With at most 512 candidates, at most 64
+ * segments of up to 19,456 values (a vocabulary up to 1,245,184) and segments x candidates <= 4,096, the row is
+ * cut into segments drawn by separate workgroups of one launch, and the row's last segment to finish merges them
  * (workspace: nvs_markov_draw_workspace_size bytes, no initialisation; row_counters: int32 [batch], zero on the
- * first call and left zero by every call, shared only by calls ordered on one stream); above 512 one workgroup
+ * first call and left zero by every call, shared only by calls ordered on one stream); otherwise one workgroup
  * draws each row, needs no workspace or counters, and takes no bias (add it first).
  * The rows of a draft block are sequential launches because each row's bias depends on the token drawn before it. */
 int nvs_markov_draw_workspace_size(int64_t batch, int64_t vocab, int num_candidates, size_t* bytes);
