@@ -4,7 +4,7 @@ The Markov bias is a lookup table by previous token (as the reference's tests/te
 so the GPU and the CPU oracle add identical biases whenever they drew identical tokens.
 Bar: drafts bit-exact, candidate ids bit-exact, the number of kept candidates equal, probabilities within 1e-5 of
 their value (the kernel's exp and its sum order differ from torch's softmax). Cases: the reference's propose tests,
-random rows at V = 4,096 (fp32) and 151,936 (bf16) with mixed temperatures / top-k / top-p, ties at the cut inside
+random rows at V = 4,096 (fp32), 151,936 (bf16) and 32,000 (fp16) with mixed temperatures / top-k / top-p, ties at the cut inside
 and beyond the candidates (the kernel's ordered tie pass), a dense batch (a row without top-k), and the sparse rows
 scattered back to the reference's dense q.
 """
@@ -79,7 +79,8 @@ def test_reference_propose_cases(device):
     assert torch.equal(dense > 0, want[1] > 0) and torch.allclose(dense, want[1], rtol=1e-5, atol=1e-7)
 
 
-@pytest.mark.parametrize("vocab, dtype, batch", [(4096, torch.float32, 16), (151936, torch.bfloat16, 8)])
+@pytest.mark.parametrize("vocab, dtype, batch", [(4096, torch.float32, 16), (151936, torch.bfloat16, 8),
+                                                 (32000, torch.float16, 8)])
 def test_random_rows_match_the_oracle(device, vocab, dtype, batch):
     log_case(f"markov rows: random V={vocab} {dtype} B={batch}")
     g = torch.Generator().manual_seed(vocab)

@@ -162,6 +162,7 @@ def probs_params(n, vocab, top_k, top_p, temp, seed, dtype=torch.float32, sigma=
     ("topk_mixed_topp", [64, 5, 1, 20], [0.9, 1.0, 0.5, 0.3], [0.7, 1.0, 1.3], torch.float32),
     ("topk0_rows", [0, 64, 0, 3], [1.0], [1.0, 0.5], torch.float32),
     ("bf16_ties", [64, 50], [1.0, 0.8], [1.0], torch.bfloat16),
+    ("fp16_mixed", [64, 20, 0, 5], [1.0, 0.9], [1.0, 0.8], torch.float16),
     ("topk1000", [1000, 700], [1.0, 0.95], [1.0], torch.float32),
 ])
 @pytest.mark.parametrize("vocab", [4099, 5000, 151936])   # 4099: rows that are not 16-byte aligned
@@ -267,6 +268,11 @@ def draft_probs(draft_logits, temps, tk, tp):
                                        verified_lens=[1, 8, 3, 5, 2, 7, 4, 6], temperature=[0.7, 1.0, 1.3, 1.0] * 2)),
     ("no_topk_odd_vocab", dict(batch=4, num_drafts=3, vocab=32001, top_k=0, temperature=[0.7, 1.0] * 2)),
     ("bf16_logits", dict(batch=8, num_drafts=7, vocab=151936, logits_dtype=torch.bfloat16)),
+    # an fp16 model's logits (model_runner.py:55-57 builds the model in hf_config.dtype)
+    ("fp16_logits_topp_temps", dict(batch=8, num_drafts=7, vocab=151936, logits_dtype=torch.float16,
+                                    top_k=[64, 20, 5, 64] * 2, top_p=[0.9, 1.0, 0.6, 0.95] * 2,
+                                    temperature=[0.7, 1.0, 1.5, 1.0] * 2, verified_lens=[1, 8, 3, 5, 2, 7, 4, 6])),
+    ("no_topk_fp16", dict(batch=8, num_drafts=7, vocab=32000, top_k=0, logits_dtype=torch.float16)),
     ("small_sigma", dict(batch=8, num_drafts=7, vocab=151936, sigma=0.5)),
 ])
 def test_fused_accept_is_bit_exact(device, name, kwargs):
