@@ -1701,8 +1701,9 @@ __global__ __launch_bounds__(kSelThreads, 4) void markov_draw_kernel(MarkovSplit
     const int64_t row_tk = a.top_k[b];
     // What the merge needs besides the lists, requested first (before the segment's keys, which then cannot delay
     // them): used only by the row's last segment.
-    const float noise_c = threadIdx.x < a.n_cand ? a.noise[b * a.noise_stride + threadIdx.x] : 1.f;
-    const float noise_c64 = threadIdx.x + 64 < a.n_cand ? a.noise[b * a.noise_stride + threadIdx.x + 64] : 1.f;
+    const int tid = static_cast<int>(threadIdx.x);
+    const float noise_c = tid < a.n_cand ? a.noise[b * a.noise_stride + tid] : 1.f;
+    const float noise_c64 = tid + 64 < a.n_cand ? a.noise[b * a.noise_stride + tid + 64] : 1.f;
     const float row_top_p = a.has_top_p ? a.top_p[b] : 1.f;
     const int es = nvs::dtype_size(DT);
     const char* row = static_cast<const char*>(a.logits) + (b * a.row_stride + e_lo) * es;
@@ -1805,7 +1806,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void markov_draw_kernel(MarkovSplit
 #pragma unroll
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t cand = wb | (1u << bit);
-        if (__popcll(__ballot(tmax >= cand)) >= rw) wb = cand;
+        if (static_cast<int>(__popcll(__ballot(tmax >= cand))) >= rw) wb = cand;
     }
     const uint32_t wmaxk = wave_max_u32(tmax);
     if (lane_id() == 0) {
@@ -2282,7 +2283,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
 #pragma unroll
                 for (int bit = 31; bit >= 0; --bit) {
                     const uint32_t cand = bound | (1u << bit);
-                    if (__popcll(__ballot(tmax >= cand)) >= rw) bound = cand;
+                    if (static_cast<int>(__popcll(__ballot(tmax >= cand))) >= rw) bound = cand;
                 }
             }
             if (lane == 0) sh.ured[wave] = bound;
