@@ -109,6 +109,21 @@ def test_torch_fp32_restatement_matches_f64():
     np.testing.assert_allclose(got.numpy(), want, rtol=1e-5, atol=1e-5)
 
 
+def test_config_c1_fp32_through_the_oracle():
+    """C1 as specified: fp32 q/K/V, 16 q / 8 kv heads, one row of 8 verify positions over 1,024 keys in four
+    permuted 256-key blocks plus the zero pad block. The fp32 restatement (the CPU baseline's path) against the fp64
+    brute force, and the row's first position (which sees keys 0..1016) against the dense brute force."""
+    c = wl.config_c1()
+    assert c.q.dtype == torch.float32 and c.k_cache.shape == (5, 256, 8, 128)
+    assert sorted(c.block_tables[0, :4].tolist()) == [0, 1, 2, 3] and c.block_tables[0, :4].tolist() != [0, 1, 2, 3]
+    want = ref.paged_attention_f64(c.q, c.k_cache, c.v_cache, c.block_tables, c.rows, c.scale, True)
+    got = ref.paged_attention_t32(c.q, c.k_cache, c.v_cache, c.block_tables, c.rows, c.scale, True)
+    np.testing.assert_allclose(got.numpy()[:8], want[:8], rtol=1e-5, atol=1e-5)
+    one = case([1], [1017], h=16, hkv=8, d=128, bs=256)
+    one.q, one.k_cache, one.v_cache, one.block_tables = c.q[:1], c.k_cache, c.v_cache, c.block_tables
+    np.testing.assert_allclose(want[:1], dense_bruteforce(one), rtol=1e-10, atol=1e-12)
+
+
 def test_padding_rows_read_the_zero_pad_block():
     c = wl.verify_attention_case([3, 2], [10, 20], 4, 2, 16, block_size=8, pad_tokens_to=8, max_query_len=8)
     assert c.real_rows == 2 and len(c.q_lens) == 3 and sum(c.q_lens) == 8
