@@ -27,6 +27,7 @@
 #include "spec_accept.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 namespace {
 
@@ -1748,50 +1749,70 @@ __global__ __launch_bounds__(kSelThreads, 4) void markov_draw_kernel(MarkovSplit
     }
     uint32_t tmax = 0u;   // this thread's largest key
     // The thread's keys stay in registers. Register slot q holds element (threadIdx.x + (q / W) * kSelThreads) *
-    // W + q % W, so index order is (q / W, thread, q % W); the valid slots are a prefix, q < qlim.
+    // W + q % W, so index order is (q / W, thread, q % W); the valid slots are a prefix, q < qlim. Slots past the
+    // segment hold key 0, which leaves tmax as it is; every later use of a slot also checks q < qlim.
     uint32_t kr[kMaxPc * W];
+    int lim[kMaxPc];   // valid elements of each of the thread's pieces (0 past the segment)
     int qlim = 0;
 #pragma unroll
     for (int j = 0; j < kMaxPc; ++j) {
         const int pc = static_cast<int>(threadIdx.x) + j * kSelThreads;
-        const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-        float v[W];
-        float bv[W];
-        if constexpr (DT == NVS_DTYPE_F32) {
+        lim[j] = max(0, min(W, n - pc * W));
+        if (lim[j] > 0) qlim = j * W + lim[j];
+    }
+    // The temperature and the segment's shape are the same for the whole workgroup: one branch picks the loop,
+    // rather than a select per key that would run the division for unit temperatures too.
+    auto convert = [&](auto unit_c, auto whole_c) {
+        constexpr bool kUnit = decltype(unit_c)::value;     // temperature 1: no division
+        constexpr bool kWhole = decltype(whole_c)::value;   // every piece of the segment whole (n % W == 0)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v[c] = __uint_as_float(w4[c]);
-        } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                v[2 * c] = half_of<DT>(w4[c], 0);
-                v[2 * c + 1] = half_of<DT>(w4[c], 1);
-            }
-        }
-        if constexpr (BIAS) {
-            const uint32_t b4[4] = {braw[j].x, braw[j].y, braw[j].z, braw[j].w};
+        for (int j = 0; j < kMaxPc; ++j) {
+            const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+            float v[W];
+            float bv[W];
             if constexpr (DT == NVS_DTYPE_F32) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) bv[c] = __uint_as_float(b4[c]);
+                for (int c = 0; c < 4; ++c) v[c] = __uint_as_float(w4[c]);
             } else {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    bv[2 * c] = half_of<DT>(b4[c], 0);
-                    bv[2 * c + 1] = half_of<DT>(b4[c], 1);
+                    v[2 * c] = half_of<DT>(w4[c], 0);
+                    v[2 * c + 1] = half_of<DT>(w4[c], 1);
                 }
             }
-        }
+            if constexpr (BIAS) {
+                const uint32_t b4[4] = {braw[j].x, braw[j].y, braw[j].z, braw[j].w};
+                if constexpr (DT == NVS_DTYPE_F32) {
 #pragma unroll
-        for (int c = 0; c < W; ++c) {
-            const int i = pc * W + c;
-            float x = v[c];
-            if constexpr (BIAS) x = round_to_dtype<DT>(x + bv[c]);
-            const uint32_t key = sel_key(scale_logit(x, temp, unit_temp));
-            kr[j * W + c] = key;
-            if (pc < pieces && i < n) {
+                    for (int c = 0; c < 4; ++c) bv[c] = __uint_as_float(b4[c]);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        bv[2 * c] = half_of<DT>(b4[c], 0);
+                        bv[2 * c + 1] = half_of<DT>(b4[c], 1);
+                    }
+                }
+            }
+            const bool piece_in = lim[j] > 0;
+#pragma unroll
+            for (int c = 0; c < W; ++c) {
+                float x = v[c];
+                if constexpr (BIAS) x = round_to_dtype<DT>(x + bv[c]);
+                if constexpr (!kUnit) x = x / temp;
+                const bool in = kWhole ? piece_in : (c < lim[j]);
+                const uint32_t key = in ? sel_key(x) : 0u;
+                kr[j * W + c] = key;
                 tmax = max(tmax, key);
-                qlim = j * W + c + 1;
             }
         }
+    };
+    const bool whole = (n % W) == 0;
+    if (unit_temp) {
+        if (whole) convert(std::true_type{}, std::true_type{});
+        else convert(std::true_type{}, std::false_type{});
+    } else {
+        if (whole) convert(std::false_type{}, std::true_type{});
+        else convert(std::false_type{}, std::false_type{});
     }
     __syncthreads();
     // The segment's want-th largest key, want = the row's top-k window (a row without top-k: max_top_k) or the

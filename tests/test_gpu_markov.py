@@ -4,7 +4,8 @@ The Markov bias is a lookup table by previous token (as the reference's tests/te
 so the GPU and the CPU oracle add identical biases whenever they drew identical tokens.
 Bar: drafts bit-exact, candidate ids bit-exact, the number of kept candidates equal, probabilities within 1e-5 of
 their value (the kernel's exp and its sum order differ from torch's softmax). Cases: the reference's propose tests,
-random rows at V = 4,096 (fp32), 151,936 (bf16) and 32,000 (fp16) with mixed temperatures / top-k / top-p, ties at the cut inside
+random rows at V = 4,096 (fp32), 151,936 (bf16) and 32,000 (fp16) with mixed temperatures / top-k / top-p,
+vocabularies that end inside a 16-byte piece (padded and unpadded rows), ties at the cut inside
 and beyond the candidates (the kernel's ordered tie pass), a dense batch (a row without top-k), and the sparse rows
 scattered back to the reference's dense q.
 """
@@ -27,12 +28,21 @@ def sampling(device, temps, top_k, top_p):
     return ns.SamplingTensors(t, k, p, int(k.max()), bool((p < 1).any()), bool((k > 0).all()))
 
 
-def run_both(device, logits, anchors, table, st, seed=0):
-    """The product's sample_markov on the GPU and the oracle on the CPU with the same noise."""
+def run_both(device, logits, anchors, table, st, seed=0, pad=0):
+    """The product's sample_markov on the GPU and the oracle on the CPU with the same noise. With pad > 0 the
+    device logits and bias rows sit in rows pad elements wider (row strides the vocabulary does not give)."""
     bias = lambda prev: table[prev % table.shape[0]]
     gen = torch.Generator(device=device).manual_seed(seed)
-    lg = logits.to(device)
-    tab = table.to(device)
+    if pad:
+        lg = torch.zeros(*logits.shape[:-1], logits.shape[-1] + pad, dtype=logits.dtype, device=device)
+        lg = lg[..., :logits.shape[-1]]
+        lg.copy_(logits)
+        tab = torch.zeros(table.shape[0], table.shape[1] + pad, dtype=table.dtype, device=device)
+        tab = tab[:, :table.shape[1]]
+        tab.copy_(table)
+    else:
+        lg = logits.to(device)
+        tab = table.to(device)
     drafts, q = nm.sample_markov(lg, anchors.to(device), st, lambda prev: tab[prev % tab.shape[0]], gen)
     torch.cuda.synchronize()
     batch, k, vocab = logits.shape
@@ -94,6 +104,29 @@ def test_random_rows_match_the_oracle(device, vocab, dtype, batch):
     drafts, q, want = run_both(device, logits, anchors, table, st, seed=1)
     assert torch.equal(drafts, want[0]), f"drafts differ at {(drafts != want[0]).nonzero()[:5].tolist()}"
     check_candidates(q, want, "random rows")
+
+
+@pytest.mark.parametrize("vocab, dtype, pad", [
+    (32003, torch.bfloat16, 5),    # element loads (V is no whole number of 16-byte pieces); the last segment
+    (32003, torch.bfloat16, 0),    # ends inside a piece of 8, with rows padded to 32,008 and unpadded
+    (4099, torch.float32, 5),      # one segment ending inside a piece of 4
+    (4099, torch.float16, 0),
+    (32000, torch.bfloat16, 8),    # whole pieces: 16-byte loads at a row stride other than V
+])
+def test_vocabulary_ending_inside_a_piece_and_padded_rows(device, vocab, dtype, pad):
+    log_case(f"markov rows: V={vocab} {dtype} row pad {pad}")
+    g = torch.Generator().manual_seed(vocab + pad)
+    batch = 8
+    logits = (torch.randn(batch, 4, vocab, generator=g) * 3).to(dtype)
+    logits[:, :, -2:] += 12.0   # the last elements, past the final whole piece, among the candidates
+    table = (torch.randn(16, vocab, generator=g) * 2).to(dtype)
+    st = sampling(device, [1.0, 0.7, 1.3, 1.0] * 2, [20, 5, 50, 1] * 2, [1.0, 0.8, 0.95, 1.0] * 2)
+    anchors = torch.randint(0, vocab, (batch,), generator=g)
+    drafts, q, want = run_both(device, logits, anchors, table, st, seed=3, pad=pad)
+    assert torch.equal(drafts, want[0]), f"drafts differ at {(drafts != want[0]).nonzero()[:5].tolist()}"
+    check_candidates(q, want, f"V={vocab} pad {pad}")
+    ids = q.ids.cpu()
+    assert bool(((ids == vocab - 1) | (ids == vocab - 2)).any()), "the last elements were never candidates"
 
 
 @pytest.mark.parametrize("vocab, dtype, top_k", [
