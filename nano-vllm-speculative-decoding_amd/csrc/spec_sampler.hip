@@ -1816,8 +1816,9 @@ __global__ __launch_bounds__(kSelThreads, 4) void markov_draw_kernel(MarkovSplit
     }
     __syncthreads();
     // The segment's want-th largest key, want = the row's top-k window (a row without top-k: max_top_k) or the
-    // segment's length. A lower bound first: each wave's ceil(want / 8)-th largest lane maximum (one ballot per
-    // bit), the smallest over the waves; every wave has that many lanes holding a key at or above it, so at least
+    // segment's length. A lower bound first: each wave's ceil(want / 8)-th largest lane maximum, rounded down to a
+    // multiple of 2^16 (one ballot for each of the upper 16 bits: exact for 16-bit logits, whose keys carry no
+    // more), the smallest over the waves; every wave has that many lanes holding a key at or above it, so at least
     // `want` keys are.
     const int K = static_cast<int>(min(static_cast<int64_t>(a.max_top_k), a.vocab));
     const int want = static_cast<int>(min(min(row_tk > 0 ? row_tk : static_cast<int64_t>(K), static_cast<int64_t>(K)),
@@ -1825,7 +1826,7 @@ __global__ __launch_bounds__(kSelThreads, 4) void markov_draw_kernel(MarkovSplit
     const int rw = (want + kSelWaves - 1) / kSelWaves;   // <= 64: K <= n_cand <= kSplitMaxCand
     uint32_t wb = 0u;
 #pragma unroll
-    for (int bit = 31; bit >= 0; --bit) {
+    for (int bit = 31; bit >= 16; --bit) {
         const uint32_t cand = wb | (1u << bit);
         if (static_cast<int>(__popcll(__ballot(tmax >= cand))) >= rw) wb = cand;
     }
@@ -1851,17 +1852,21 @@ __global__ __launch_bounds__(kSelThreads, 4) void markov_draw_kernel(MarkovSplit
     // (key, index) pairs to the pair space: each lane's count, one prefix over the wave and one reservation per
     // wave, then the lane's keys in order.
     uint64_t* list = pair_buf(sh);
-    {
+    // With a bound above key 0 the slots past the segment (key 0) fail the test by themselves; only a bound of 0
+    // needs q < qlim as well.
+    auto short_list = [&](auto all_c) {
+        constexpr bool kCheckSlot = decltype(all_c)::value;
+        auto passes = [&](int q) { return (!kCheckSlot || q < qlim) && kr[q] >= lo; };
         int mine = 0;
 #pragma unroll
-        for (int q = 0; q < kMaxPc * W; ++q) mine += (q < qlim && kr[q] >= lo) ? 1 : 0;
+        for (int q = 0; q < kMaxPc * W; ++q) mine += passes(q) ? 1 : 0;
         const int incl = wave_scan_incl_dpp(mine);
         int base = 0;
         if (lane_id() == 63 && incl > 0) base = atomicAdd(&sh.count, incl);
-        int p = __shfl(base, 63) + incl - mine;
+        int p = __builtin_amdgcn_readlane(base, 63) + incl - mine;
 #pragma unroll
         for (int q = 0; q < kMaxPc * W; ++q) {
-            if (q < qlim && kr[q] >= lo) {
+            if (passes(q)) {
                 if (p < kShortCap) {
                     const int i = (static_cast<int>(threadIdx.x) + (q / W) * kSelThreads) * W + q % W;
                     list[p] = (static_cast<uint64_t>(kr[q]) << 32) | (0xffffffffu - static_cast<uint32_t>(e_lo + i));
@@ -1869,7 +1874,9 @@ __global__ __launch_bounds__(kSelThreads, 4) void markov_draw_kernel(MarkovSplit
                 ++p;
             }
         }
-    }
+    };
+    if (lo > 0u) short_list(std::false_type{});
+    else short_list(std::true_type{});
     __syncthreads();
     const int nl = sh.count;
     if (nl <= kShortCap) {
