@@ -1464,11 +1464,15 @@ __device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float nois
     // every load issued before any is used: one round trip to the coherence point (total <= kPairCap / 2 pairs,
     // n_seg <= 64 counts, one per lane of every wave)
     constexpr int kPer = kPairCap / 2 / kSelThreads;
+    const int rounds = (total + kSelThreads - 1) / kSelThreads;   // the rounds of slots that exist (uniform)
     uint64_t got[kPer];
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
-        const int i = min(static_cast<int>(threadIdx.x) + r * kSelThreads, total - 1);
-        got[r] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        got[r] = 0ull;
+        if (r < rounds) {
+            const int i = min(static_cast<int>(threadIdx.x) + r * kSelThreads, total - 1);
+            got[r] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     const int cnt_raw = __hip_atomic_load(a.seg_counts + b * a.n_seg + min(lane, a.n_seg - 1), __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
@@ -1482,6 +1486,7 @@ __device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float nois
         // advance eight lists at a time (one LDS round trip per halving for all eight).
 #pragma unroll
         for (int r = 0; r < kPer; ++r) {
+            if (r >= rounds) break;
             const int e = static_cast<int>(threadIdx.x) + r * kSelThreads;
             const int li = e / C;
             const int i = e - li * C;
@@ -1533,6 +1538,7 @@ __device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float nois
         // the lists at their slots, zero past each count (zeros sort below every pair)
 #pragma unroll
         for (int r = 0; r < kPer; ++r) {
+            if (r >= rounds) break;
             const int e = static_cast<int>(threadIdx.x) + r * kSelThreads;
             const int li = e / C;
             const int i = e - li * C;
