@@ -565,17 +565,12 @@ __device__ float top_p_threshold(SelShared& sh, int rank, int K, float top_p, fl
         const int l = lane_id();
         const float m = nvs::key_float(sh.sortbuf[0]);
         const int per = (rank + 63) / 64;
-        // e[] in registers: every loop over it unrolled, its slots past per skipped
         float e[16];
         float lsum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            e[i] = 0.f;
-            if (i < per) {
-                const int r = l * per + i;
-                e[i] = (r < rank) ? expf(nvs::key_float(sh.sortbuf[r]) - m) : 0.f;
-                lsum += e[i];
-            }
+        for (int i = 0; i < per && i < 16; ++i) {
+            const int r = l * per + i;
+            e[i] = (r < rank) ? expf(nvs::key_float(sh.sortbuf[r]) - m) : 0.f;
+            lsum += e[i];
         }
         const float total = wave_sum(lsum);
         // The nucleus cumsum as torch's CPU cumsum of fp32 computes it: accumulated in double, each prefix rounded
@@ -583,20 +578,16 @@ __device__ float top_p_threshold(SelShared& sh, int rank, int K, float top_p, fl
         // early on a peaked row and would cut entries the reference keeps. Local sums first, then the lanes'
         // exclusive prefix.
         double loc = 0.0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            if (i < per) {
-                e[i] = e[i] / total;
-                loc += static_cast<double>(e[i]);
-            }
+        for (int i = 0; i < per && i < 16; ++i) {
+            e[i] = e[i] / total;
+            loc += static_cast<double>(e[i]);
         }
         const double incl = wave_scan_incl_f64(loc);
         double run = incl - loc;
         int kept = 0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < per && i < 16; ++i) {
             const int r = l * per + i;
-            if (i < per && r < rank) {
+            if (r < rank) {
                 run += static_cast<double>(e[i]);
                 const float before = static_cast<float>(run) - e[i];
                 kept += (before < top_p) ? 1 : 0;
