@@ -26,18 +26,18 @@ import time
 HBM_PEAK_GBS = 8000.0
 METRIC = "verify-attn µs/layer & HBM GB/s (% of 8 TB/s) at B=64, 8 q, 3k ctx"
 
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (one counter per run) at commit
-# 628323f, each scaled by what the counter reads for the 1 GiB copy probe (FETCH_SIZE x 1.99995, WRITE_SIZE x 1.0);
-# the runs and their numbers are in profiles/hbm_traffic_pmc_verify_attention_and_spec_accept.md. Re-measure after a
-# kernel change.
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (one counter per run) at the commit
+# beside each entry, each scaled by what the counter reads for the 1 GiB copy probe (FETCH_SIZE x 1.99995,
+# WRITE_SIZE x 1.0); the runs and their numbers are in profiles/hbm_traffic_pmc_verify_attention_and_spec_accept.md.
+# Re-measure after a kernel change.
 MEASURED_TRAFFIC = {
     "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200": 789_697_462,              # head-major caches, 628323f
     "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_token_major": 789_712_493,  # 628323f
     "verify_attention_qwen3_8b_b64_varlen_q1_8_ctx2800_3200_kv_interleaved": 789_712_021,  # 628323f
     "spec_accept_b64_k7_v151936_fp32_topk64": 320_037_489,                              # 628323f
-    "markov_draw_b64_v151936_bf16_rank64": 40_277_485,                                  # 628323f
+    "markov_draw_b64_v151936_bf16_rank64": 40_235_723,                                  # f8d0a8b
 }
-MEASURED_AT = "628323f"
+MEASURED_AT = "628323f"   # the headline (attention) entry
 
 
 def log(msg: str) -> None:
