@@ -565,31 +565,30 @@ __device__ float top_p_threshold(SelShared& sh, int rank, int K, float top_p, fl
         const int l = lane_id();
         const float m = nvs::key_float(sh.sortbuf[0]);
         const int per = (rank + 63) / 64;
-        float e[16];
-        float lsum = 0.f;
-        for (int i = 0; i < per && i < 16; ++i) {
+        // each lane's entries r = l * per + i, recomputed in every loop below rather than kept in a per-lane array
+        // (indexed by a runtime i it would live in private memory); expf of the same input gives the same bits
+        auto entry = [&](int i) {
             const int r = l * per + i;
-            e[i] = (r < rank) ? expf(nvs::key_float(sh.sortbuf[r]) - m) : 0.f;
-            lsum += e[i];
-        }
+            return (r < rank) ? expf(nvs::key_float(sh.sortbuf[r]) - m) : 0.f;
+        };
+        float lsum = 0.f;
+        for (int i = 0; i < per && i < 16; ++i) lsum += entry(i);
         const float total = wave_sum(lsum);
         // The nucleus cumsum as torch's CPU cumsum of fp32 computes it: accumulated in double, each prefix rounded
         // to float, then the float subtraction of the entry (spec_sampler.py:91). An fp32 running sum reaches 1.0
         // early on a peaked row and would cut entries the reference keeps. Local sums first, then the lanes'
         // exclusive prefix.
         double loc = 0.0;
-        for (int i = 0; i < per && i < 16; ++i) {
-            e[i] = e[i] / total;
-            loc += static_cast<double>(e[i]);
-        }
+        for (int i = 0; i < per && i < 16; ++i) loc += static_cast<double>(entry(i) / total);
         const double incl = wave_scan_incl_f64(loc);
         double run = incl - loc;
         int kept = 0;
         for (int i = 0; i < per && i < 16; ++i) {
             const int r = l * per + i;
             if (r < rank) {
-                run += static_cast<double>(e[i]);
-                const float before = static_cast<float>(run) - e[i];
+                const float e = entry(i) / total;
+                run += static_cast<double>(e);
+                const float before = static_cast<float>(run) - e;
                 kept += (before < top_p) ? 1 : 0;
             }
         }
@@ -1505,31 +1504,34 @@ __device__ void markov_merge_row(const MarkovSplitArgs& a, int64_t b, float nois
         if (t < n_all) {
             const uint64_t x = all[t];
             int above = t - own_start;   // its place in its own list
+            // The count of a list's pairs above x (a prefix: the list is descending) by binary lifting: steps top,
+            // top / 2, ..., 1, where top is the largest power of two not above the longest list, add up to any
+            // count. A step is taken when the pair it lands on is inside the list and above x; the pairs it reads
+            // past a list stay inside the pair space (at most n_all + 2 * longest < kPairCap / 2) and are unused.
+            int top = 1;
+            while (2 * top <= longest) top *= 2;
             for (int g0 = 0; g0 < a.n_seg; g0 += 8) {
-                int lo[8], hi[8], base[8];
+                int pos[8], lim[8], base[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     const int l = min(g0 + u, a.n_seg - 1);
                     const int c_l = __builtin_amdgcn_readlane(cnt, l);
                     base[u] = __builtin_amdgcn_readlane(cincl, l) - c_l;
-                    lo[u] = 0;
-                    hi[u] = (g0 + u < a.n_seg && g0 + u != own) ? c_l : 0;
+                    pos[u] = 0;
+                    lim[u] = (g0 + u < a.n_seg && g0 + u != own) ? c_l : 0;
                 }
-                for (int len = longest; len > 0; len >>= 1) {   // floor(log2 longest) + 1 halvings empty them
+                for (int step = top; step > 0; step >>= 1) {
                     uint64_t v[8];
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) v[u] = all[base[u] + min((lo[u] + hi[u]) >> 1, max(hi[u] - 1, 0))];
+                    for (int u = 0; u < 8; ++u) v[u] = all[base[u] + pos[u] + step - 1];   // every read, then the tests
 #pragma unroll
                     for (int u = 0; u < 8; ++u) {
-                        const int mid = (lo[u] + hi[u]) >> 1;
-                        const bool open = lo[u] < hi[u];
-                        const bool gt = v[u] > x;
-                        lo[u] = (open && gt) ? mid + 1 : lo[u];
-                        hi[u] = (open && !gt) ? mid : hi[u];
+                        const bool take = (pos[u] + step - 1 < lim[u]) & (v[u] > x);
+                        pos[u] += take ? step : 0;
                     }
                 }
 #pragma unroll
-                for (int u = 0; u < 8; ++u) above += lo[u];
+                for (int u = 0; u < 8; ++u) above += pos[u];
             }
             if (above < C) pairs[above] = x;
         }
