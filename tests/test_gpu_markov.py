@@ -5,7 +5,7 @@ so the GPU and the CPU oracle add identical biases whenever they drew identical 
 Bar: drafts bit-exact, candidate ids bit-exact, the number of kept candidates equal, probabilities within 1e-5 of
 their value (the kernel's exp and its sum order differ from torch's softmax). Cases: the reference's propose tests,
 random rows at V = 4,096 (fp32), 151,936 (bf16) and 32,000 (fp16) with mixed temperatures / top-k / top-p,
-vocabularies that end inside a 16-byte piece (padded and unpadded rows), ties at the cut inside
+vocabularies that end inside a 16-byte piece (padded and unpadded rows), rows cut into 11 and 62 segments, ties at the cut inside
 and beyond the candidates (the kernel's ordered tie pass), a dense batch (a row without top-k), and the sparse rows
 scattered back to the reference's dense q.
 """
@@ -104,6 +104,22 @@ def test_random_rows_match_the_oracle(device, vocab, dtype, batch):
     drafts, q, want = run_both(device, logits, anchors, table, st, seed=1)
     assert torch.equal(drafts, want[0]), f"drafts differ at {(drafts != want[0]).nonzero()[:5].tolist()}"
     check_candidates(q, want, "random rows")
+
+
+def test_segments_near_the_limit_match_the_oracle(device):
+    """V = 1,200,000 cuts each row into 62 segments (the split draw allows 64, and segments x candidates <= 4,096,
+    so top-k <= 2 here): the merge's counts run over eight groups of lists."""
+    vocab = 1_200_000
+    log_case(f"markov rows: V={vocab} bf16, 62 segments")
+    g = torch.Generator().manual_seed(62)
+    batch = 4
+    logits = (torch.randn(batch, 2, vocab, generator=g) * 3).to(torch.bfloat16)
+    table = (torch.randn(4, vocab, generator=g) * 2).to(torch.bfloat16)
+    st = sampling(device, [1.0, 0.8, 1.0, 1.3], [2, 1, 2, 2], [1.0, 1.0, 0.9, 1.0])
+    anchors = torch.randint(0, vocab, (batch,), generator=g)
+    drafts, q, want = run_both(device, logits, anchors, table, st, seed=4)
+    assert torch.equal(drafts, want[0]), f"drafts differ at {(drafts != want[0]).nonzero()[:5].tolist()}"
+    check_candidates(q, want, "62 segments")
 
 
 @pytest.mark.parametrize("vocab, dtype, pad", [
