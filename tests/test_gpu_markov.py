@@ -5,9 +5,9 @@ so the GPU and the CPU oracle add identical biases whenever they drew identical 
 Bar: drafts bit-exact, candidate ids bit-exact, the number of kept candidates equal, probabilities within 1e-5 of
 their value (the kernel's exp and its sum order differ from torch's softmax). Cases: the reference's propose tests,
 random rows at V = 4,096 (fp32), 151,936 (bf16) and 32,000 (fp16) with mixed temperatures / top-k / top-p,
-vocabularies that end inside a 16-byte piece (padded and unpadded rows), rows cut into 11 and 62 segments, ties at the cut inside
-and beyond the candidates (the kernel's ordered tie pass), a dense batch (a row without top-k), and the sparse rows
-scattered back to the reference's dense q.
+vocabularies that end inside a 16-byte piece (padded and unpadded rows), rows cut into 11 and 62 segments, ties at
+the cut inside and beyond the candidates (the kernel's ordered tie pass), a dense batch (a row without top-k), and
+the sparse rows scattered back to the reference's dense q.
 """
 import pytest
 import torch
