@@ -983,19 +983,32 @@ __device__ void build_q_hash(const SelArgs& a, int64_t slot, SelShared& sh) {
     __syncthreads();
 }
 
-// The same hash built by one wave alone (the wave-0 finish, while the other waves wait): LDS operations of one wave
-// take effect in program order, so the lookups that follow see every insert.
-__device__ void build_q_hash_wave(const SelArgs& a, int64_t slot, SelShared& sh) {
+// The row's first 128 candidates (lane and lane + 64), requested by the wave-0 finish before its threshold so that
+// their round trip overlaps it; id -1 past the row's candidates.
+__device__ __forceinline__ void load_q_row_head(const SelArgs& a, int64_t slot, int32_t (&id)[2], float (&pr)[2]) {
+    const int32_t* ids = a.q_ids + slot * a.q_stride;
+    const float* probs = a.q_probs + slot * a.q_stride;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = lane_id() + 64 * h;
+        id[h] = c < a.q_cand ? ids[c] : -1;
+        pr[h] = c < a.q_cand ? probs[c] : 0.f;
+    }
+}
+
+// The same hash built by one wave alone (the wave-0 finish, while the other waves wait), from the row's first 128
+// candidates already in registers and the rest loaded here: LDS operations of one wave take effect in program order,
+// so the lookups that follow see every insert. Each id is in the row once, so the order of inserts does not matter.
+__device__ __forceinline__ void build_q_hash_wave(const SelArgs& a, int64_t slot, SelShared& sh, int32_t id0,
+                                                  float pr0, int32_t id1, float pr1) {
     uint32_t* keys = &sh.whist[0][0];
     uint32_t* vals = keys + kQHash;
     const int32_t* ids = a.q_ids + slot * a.q_stride;
     const float* probs = a.q_probs + slot * a.q_stride;
     for (int i = lane_id(); i < kQHash; i += 64) keys[i] = 0u;
     compiler_fence_s();
-    for (int c = lane_id(); c < a.q_cand; c += 64) {
-        const int32_t id = ids[c];
-        const float pr = probs[c];
-        if (id < 0) continue;
+    auto insert = [&](int32_t id, float pr) {
+        if (id < 0) return;
         const uint32_t key = static_cast<uint32_t>(id) + 1u;
         uint32_t h = q_hash(id);
         for (int probe = 0; probe < kQHash; ++probe) {
@@ -1006,7 +1019,10 @@ __device__ void build_q_hash_wave(const SelArgs& a, int64_t slot, SelShared& sh)
             }
             h = (h + 1u) & (kQHash - 1);
         }
-    }
+    };
+    insert(id0, pr0);
+    insert(id1, pr1);
+    for (int c = lane_id() + 128; c < a.q_cand; c += 64) insert(ids[c], probs[c]);
     compiler_fence_s();
 }
 
@@ -1029,7 +1045,7 @@ __device__ float q_hash_lookup(SelShared& sh, int64_t token) {
 // over its kept set, or, for a row that does not truncate, a race over the whole vocabulary run here. The caller
 // has acquired the other positions' records (count_position).
 template <int DT>
-__device__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L, SelShared& sh) {
+__device__ __forceinline__ void finish_row(const SelArgs& a, int64_t b, int64_t start, int64_t L, SelShared& sh) {
     const int kd = a.k;
     if (threadIdx.x < 64) {
         // wave 0: lane i loads the record of position start + c0 + i, all in one round trip; the first position
@@ -2475,6 +2491,16 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                     kk[w] = c < n_top ? sh.sortbuf[c] : 0u;
                     ki[w] = c < n_top ? static_cast<int32_t>(sh.sortbuf[kTopCap + c]) : 0;
                 }
+                // the fused accept with q as candidate rows: the row's first candidates requested now (hashed
+                // after the threshold)
+                int32_t qh_id[2] = {-1, -1};
+                float qh_pr[2] = {0.f, 0.f};
+                if constexpr (MODE == kModeAccept) {
+                    const int64_t j = sh.loc[1], L = sh.loc[2];
+                    const bool bonus = (j >= L - 1) || (j >= a.k);
+                    if (a.q_ids != nullptr && !bonus && a.q_cand <= kQHash / 2)
+                        load_q_row_head(a, sh.loc[0] * a.k + j, qh_id, qh_pr);
+                }
                 // threshold: the largest key of the bin with at least bin_rank keys of the bin at or above it
                 const int nb_keys = sh.bin_count;
                 uint32_t cand = 0u;
@@ -2529,22 +2555,23 @@ __global__ __launch_bounds__(kSelThreads, 4) void select_kernel(SelArgs a) {
                     // space (free once the threshold is known); rows with more candidates are broadcast instead
                     const bool sparse = a.q_ids != nullptr;
                     const bool whash = sparse && !bonus && a.q_cand <= kQHash / 2;
-                    if (whash) build_q_hash_wave(a, b * kd + j, sh);
-                    float dq = dec_q;
-                    if (sparse && dec_valid) dq = whash ? q_hash_lookup(sh, dec_d) : sparse_q_wave(a, dec_slot, dec_d);
-                    if (lane == 0 && dec_valid) {
-                        const float sd = scale_logit(dec_x, temp, unit_temp);
-                        const float pd = (sel_key(sd) >= theta_key && sel_key(sd) != 0u) ? expf(sd - mu_f) / z : 0.f;
-                        acc = (dec_u * dq < pd) ? 1 : 0;
-                    }
+                    // the kept tokens' noise requested first (index 0 stands in for a pair that is not kept), so
+                    // that its round trip overlaps the q lookups below
                     const float* erow = a.noise + b * a.vocab;
-                    // every load first (index 0 stands in for a pair that is not kept), then the scores
                     float qv[kSelWaves], ev[kSelWaves];
                     int32_t tok[kSelWaves];
 #pragma unroll
                     for (int w = 0; w < kSelWaves; ++w) {
                         tok[w] = kk[w] >= theta_key ? ki[w] : 0;
                         ev[w] = erow[tok[w]];
+                    }
+                    if (whash) build_q_hash_wave(a, b * kd + j, sh, qh_id[0], qh_pr[0], qh_id[1], qh_pr[1]);
+                    float dq = dec_q;
+                    if (sparse && dec_valid) dq = whash ? q_hash_lookup(sh, dec_d) : sparse_q_wave(a, dec_slot, dec_d);
+                    if (lane == 0 && dec_valid) {
+                        const float sd = scale_logit(dec_x, temp, unit_temp);
+                        const float pd = (sel_key(sd) >= theta_key && sel_key(sd) != 0u) ? expf(sd - mu_f) / z : 0.f;
+                        acc = (dec_u * dq < pd) ? 1 : 0;
                     }
                     if (bonus) {
 #pragma unroll
